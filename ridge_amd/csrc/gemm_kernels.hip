@@ -1,0 +1,135 @@
+// gemm_kernels.hip -- instantiates the gfx950 GEMM template over the registered
+// variant table and exports the table through the C ABI in include/ridge_gemm.h.
+//
+// Counterpart of bench/kernels/gemm-mma.cu (launchVariant :19-43, kVariants
+// :55-117, numVariants/variant/printVariantTable :121-141).
+
+#include "gemm_mfma.hpp"
+#include "gemm_resources.h"
+#include "ridge_gemm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace {
+
+typedef hipError_t (*LaunchFn)(const void*, const void*, void*, int, int, int, hipStream_t);
+
+template <int BM, int BN, int BK, int WM, int WN, int S, int G>
+hipError_t launchVariant(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t stream) {
+    using T = ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>;
+    const dim3 grid((unsigned)((M / BM) * (N / BN)));
+    const dim3 block(T::kThreads);
+    hipLaunchKernelGGL((ridge::gemmMfmaKernel<BM, BN, BK, WM, WN, S, G>), grid, block, 0, stream,
+                       static_cast<const _Float16*>(A), static_cast<const _Float16*>(B),
+                       static_cast<_Float16*>(C), M, N, K);
+    return hipGetLastError();
+}
+
+struct Entry {
+    int BM, BN, BK, WM, WN, stages, groupM;
+    int ldsBytes;
+    int threads;
+    int waves;
+    LaunchFn launch;
+};
+
+#define RIDGE_VARIANT(BM, BN, BK, WM, WN, S, G)                                              \
+    Entry{BM, BN, BK, WM, WN, S, G,                                                          \
+          ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kLdsBytes,                            \
+          ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kThreads,                             \
+          ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kWaves,                               \
+          &launchVariant<BM, BN, BK, WM, WN, S, G>},
+
+const Entry kTable[] = {
+#include "gemm_variants.def"
+};
+#undef RIDGE_VARIANT
+
+constexpr int kNumVariants = int(sizeof(kTable) / sizeof(kTable[0]));
+
+bool validIndex(int i) { return i >= 0 && i < kNumVariants; }
+
+}  // namespace
+
+extern "C" {
+
+int ridge_gemm_num_variants(void) { return kNumVariants; }
+
+int ridge_gemm_get_variant(int i, ridge_gemm_variant_t* out) {
+    if (!validIndex(i) || out == nullptr) return (int)hipErrorInvalidValue;
+    const Entry& e = kTable[i];
+    ridge_gemm_variant_t v;
+    std::memset(&v, 0, sizeof(v));
+    v.BM = e.BM; v.BN = e.BN; v.BK = e.BK; v.WM = e.WM; v.WN = e.WN;
+    v.stages = e.stages; v.groupM = e.groupM;
+    v.ldsBytes = e.ldsBytes; v.threads = e.threads; v.waves = e.waves;
+    if (i < ridge_gemm_resource_count) {
+        const ridge_gemm_resources_t& r = ridge_gemm_resource_table[i];
+        v.vgprs = r.vgprs; v.agprs = r.agprs; v.sgprs = r.sgprs;
+        v.scratchBytes = r.scratchBytes; v.occupancy = r.occupancy;
+        v.regsPerThread = r.vgprs + r.agprs;
+    } else {
+        v.regsPerThread = -1;
+        v.vgprs = v.agprs = v.sgprs = v.scratchBytes = v.occupancy = -1;
+    }
+    *out = v;
+    return 0;
+}
+
+int ridge_gemm_find_variant(int BM, int BN, int BK, int WM, int WN, int stages, int groupM) {
+    for (int i = 0; i < kNumVariants; ++i) {
+        const Entry& e = kTable[i];
+        if (e.BM == BM && e.BN == BN && e.BK == BK && e.WM == WM && e.WN == WN && e.stages == stages &&
+            e.groupM == groupM)
+            return i;
+    }
+    return -1;
+}
+
+int ridge_gemm_divides(int i, int M, int N, int K) {
+    if (!validIndex(i)) return 0;
+    const Entry& e = kTable[i];
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    if (M % e.BM || N % e.BN || K % e.BK) return 0;
+    // The grid is one-dimensional and offsets inside the kernel are 32-bit.
+    if ((long long)(M / e.BM) * (N / e.BN) > 0x7fffffffLL) return 0;
+    if ((long long)e.BM * K > 0x7fffffffLL || (long long)e.BK * N > 0x7fffffffLL) return 0;
+    return 1;
+}
+
+int ridge_gemm_launch(int i, const void* A, const void* B, void* C, int M, int N, int K, void* stream) {
+    if (!ridge_gemm_divides(i, M, N, K)) return (int)hipErrorInvalidValue;
+    if (A == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15u) return (int)hipErrorInvalidValue;
+    return (int)kTable[i].launch(A, B, C, M, N, K, static_cast<hipStream_t>(stream));
+}
+
+size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {
+    std::string s = "idx,BM,BN,BK,WM,WN,stages,groupM,ldsBytes,threads,regsPerThread,waves,vgprs,agprs,sgprs,"
+                    "scratchBytes,occupancy\n";
+    char line[256];
+    for (int i = 0; i < kNumVariants; ++i) {
+        ridge_gemm_variant_t v;
+        ridge_gemm_get_variant(i, &v);
+        std::snprintf(line, sizeof(line), "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d\n", i, v.BM, v.BN,
+                      v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes, v.threads, v.regsPerThread, v.waves,
+                      v.vgprs, v.agprs, v.sgprs, v.scratchBytes, v.occupancy);
+        s += line;
+    }
+    if (buf != nullptr && cap > 0) {
+        const size_t n = s.size() < cap - 1 ? s.size() : cap - 1;
+        std::memcpy(buf, s.data(), n);
+        buf[n] = '\0';
+    }
+    return s.size();
+}
+
+const char* ridge_gemm_build_info(void) {
+    return "ridge_gemm gfx950 mfma_f32_32x32x16_f16 direct-to-LDS ring, tr16 B reads, xcd+groupM order";
+}
+
+}  // extern "C"

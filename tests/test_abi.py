@@ -1,0 +1,85 @@
+"""The C ABI library loads and exports every declared symbol, and the variant
+table is self-consistent. No GPU calls."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from ridge_amd import gemm as G
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header):
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ridge_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header", sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))))
+def test_every_declared_symbol_is_exported(header):
+    names = _declared(header)
+    assert names, header
+    libs = {
+        "ridge_gemm.h": G.LIB_PATH,
+    }
+    path = libs.get(os.path.basename(header))
+    if path is None:
+        pytest.skip("no library mapped for %s" % header)
+    L = ctypes.CDLL(path)
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_table_has_24_registered_rows_with_consistent_fields():
+    vs = G.variants()
+    assert len(vs) == 24
+    keys = [v.key() for v in vs]
+    assert len(set(keys)) == 24
+    for v in vs:
+        assert v.BM in (64, 128, 256) and v.BN in (64, 128, 256) and v.BK in (32, 64)
+        assert 2 <= v.stages <= 4
+        assert v.waves == (v.BM // v.WM) * (v.BN // v.WN)
+        assert v.threads == 64 * v.waves
+        assert v.ldsBytes == v.stages * (v.BM * v.BK + v.BK * v.BN) * 2
+        assert v.ldsBytes <= 160 * 1024
+        assert v.regsPerThread == v.vgprs + v.agprs and v.regsPerThread > 0
+        assert v.occupancy >= 1
+        assert G.find_variant(*v.key()) == v.index
+    assert G.find_variant(512, 512, 128, 64, 64, 8, 8) == -1
+
+
+def test_no_variant_spills():
+    # The reference refuses spilling kernels as ground truth (setup-box.sh:96-104).
+    assert [v.label() for v in G.variants() if v.scratchBytes != 0] == []
+
+
+def test_divisibility_and_bad_launches_are_rejected_before_any_gpu_call():
+    i = G.find_variant(256, 256, 64, 128, 128, 2, 8)
+    v = G.variant(i)
+    assert v.divides(4096, 4096, 4096)
+    assert not v.divides(4096, 4096, 4000)
+    assert not v.divides(128, 4096, 4096)
+    assert not v.divides(0, 256, 64)
+    L = G.lib()
+    # Non-dividing shape, null pointers, misaligned pointers and a bad index all
+    # return hipErrorInvalidValue without touching a device.
+    assert L.ridge_gemm_launch(i, 4096, 4096, 4096, 4096, 4096, 4000, None) == G.HIP_ERROR_INVALID_VALUE
+    assert L.ridge_gemm_launch(i, None, 4096, 4096, 256, 256, 64, None) == G.HIP_ERROR_INVALID_VALUE
+    assert L.ridge_gemm_launch(i, 4098, 4096, 4096, 256, 256, 64, None) == G.HIP_ERROR_INVALID_VALUE
+    assert L.ridge_gemm_launch(999, 4096, 4096, 4096, 256, 256, 64, None) == G.HIP_ERROR_INVALID_VALUE
+    with pytest.raises(IndexError):
+        G.variant(24)
+
+
+def test_variant_table_csv():
+    text = G.variant_table_csv()
+    lines = text.strip().splitlines()
+    assert lines[0].startswith("idx,BM,BN,BK,WM,WN,stages,groupM,ldsBytes,threads,regsPerThread")
+    assert len(lines) == 25
+    row = lines[1].split(",")
+    v = G.variant(0)
+    assert [int(x) for x in row[:11]] == [0, v.BM, v.BN, v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes,
+                                          v.threads, v.regsPerThread]

@@ -1,0 +1,161 @@
+"""GPU parity: every registered variant against the CPU f64 oracle, through the
+C ABI, on the reference's correctness shapes (bench/check-gemm.cu:83-94) and the
+BASELINE configs; bit-exact checks where the arithmetic is exact."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+import oracle as O  # noqa: E402
+from ridge_amd import gemm as G  # noqa: E402
+
+DEV = "cuda:0"
+
+# bench/check-gemm.cu:87-94.
+REFERENCE_SHAPES = [(256, 256, 64), (256, 512, 128), (512, 256, 192), (1024, 1024, 64),
+                    (1024, 512, 1024), (2048, 2048, 2048)]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    G.lib()
+    yield
+    torch.cuda.synchronize()
+
+
+def _to_dev(bits, shape):
+    return torch.from_numpy(bits.view(np.int16).reshape(shape).copy()).to(DEV).view(torch.float16)
+
+
+def _bits(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16).ravel()
+
+
+def _max_abs(bits):
+    return float(np.abs(bits.view(np.float16).astype(np.float64)).max())
+
+
+def _run(i, A, B, M, N, K):
+    C = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+    rc = G.launch(i, A, B, C, M, N, K)
+    assert rc == 0, "variant %d launch returned %d" % (i, rc)
+    torch.cuda.synchronize()
+    return C
+
+
+def test_device_fills_match_oracle_bit_exact():
+    n = (1 << 20) + 37
+    t = torch.empty(n, dtype=torch.float16, device=DEV)
+    for seed in (0x1234 + 256, 0x55AA, 0xFFFFFFFF):
+        G.fill_lcg(t, seed)
+        assert np.array_equal(_bits(t), O.lcg_fill_f16(n, seed)), seed
+    for seed in (1, 2, 0xDEADBEEFCAFEF00D):
+        G.fill_uniform(t, seed)
+        assert np.array_equal(_bits(t), O.uniform_fill_f16(n, seed)), seed
+
+
+@pytest.mark.parametrize("M,N,K", REFERENCE_SHAPES)
+def test_reference_shapes_all_dividing_variants(M, N, K):
+    print("shape %dx%dx%d" % (M, N, K), flush=True)
+    Ab = O.lcg_fill_f16(M * K, 0x1234 + M)
+    Bb = O.lcg_fill_f16(K * N, 0x9ABC + N)
+    A, B = _to_dev(Ab, (M, K)), _to_dev(Bb, (K, N))
+    # f64 where the reference affords it (M*N*K <= 2^32, check-gemm.cu:279); for
+    # larger shapes an f64 reference on a sample of 128 rows.
+    rows = np.arange(M) if M * N * K <= (1 << 32) else np.linspace(0, M - 1, 128).astype(int)
+    ref = O.gemm_f64(Ab.reshape(M, K)[rows].ravel(), Bb, len(rows), N, K)
+    tested = 0
+    for v in G.variants():
+        if not v.divides(M, N, K):
+            continue
+        print("  variant %d %s" % (v.index, v.label()), flush=True)
+        C = _run(v.index, A, B, M, N, K)
+        got = O.f16_bits_to_f32(_bits(C)).reshape(M, N)[rows]
+        ok, frob, mx, ne = O.passes(got, ref, _max_abs(Ab), _max_abs(Bb), K)
+        assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
+        tested += 1
+    assert tested > 0
+
+
+def _exact_case(M, N, K, lo, hi, seed):
+    """Integer-valued halves whose products and partial sums are exact in FP32:
+    the kernel's FP32 result is exact, so its FP16 output must equal the exact
+    integer rounded once to FP16 (nearest even)."""
+    rng = np.random.default_rng(seed)
+    A = rng.integers(lo, hi + 1, (M, K)).astype(np.float16)
+    B = rng.integers(lo, hi + 1, (K, N)).astype(np.float16)
+    # Integer sums below 2^53 are exact in float64, so BLAS gives the exact value.
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.abs(exact).max() < 2 ** 24
+    want = exact.astype(np.float16).view(np.uint16).ravel()
+    return A.view(np.uint16), B.view(np.uint16), want
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (512, 256, 192), (1024, 1024, 1024)])
+def test_small_integer_inputs_bit_exact_every_variant(M, N, K):
+    Ab, Bb, want = _exact_case(M, N, K, -3, 3, M + N + K)
+    A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+    for v in G.variants():
+        if not v.divides(M, N, K):
+            continue
+        got = _bits(_run(v.index, A, B, M, N, K))
+        bad = int(np.count_nonzero(got != want))
+        assert bad == 0, "%s: %d of %d outputs differ" % (v.label(), bad, M * N)
+
+
+def test_headline_4096_exact_integers_and_identity():
+    M = N = K = 4096
+    best = G.find_variant(256, 256, 64, 128, 128, 2, 8)
+    Ab, Bb, want = _exact_case(M, N, K, -2, 2, 4096)
+    A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+    got = _bits(_run(best, A, B, M, N, K))
+    assert np.array_equal(got, want)
+    # A = I gives C = B exactly (one exact product per output).
+    eye = torch.eye(M, dtype=torch.float16, device=DEV)
+    Bu = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(Bu, 9)
+    C = _run(best, eye, Bu, M, N, K)
+    assert torch.equal(C.view(torch.int16), Bu.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 128),
+                                   (16384, 128, 8192)])
+def test_baseline_configs_uniform_inputs(M, N, K):
+    """BASELINE.json configs with U[-1,1) inputs: every dividing variant against an
+    f64 reference on sampled rows (all rows at 1024^3)."""
+    print("baseline %dx%dx%d" % (M, N, K), flush=True)
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, 1)
+    G.fill_uniform(B, 2)
+    Ab, Bb = _bits(A), _bits(B)
+    rows = np.arange(M) if M <= 1024 else np.linspace(0, M - 1, 64).astype(int)
+    ref = O.gemm_f64(Ab.reshape(M, K)[rows].ravel(), Bb, len(rows), N, K)
+    for v in G.variants():
+        if not v.divides(M, N, K):
+            continue
+        C = _run(v.index, A, B, M, N, K)
+        got = O.f16_bits_to_f32(_bits(C)).reshape(M, N)[rows]
+        ok, frob, mx, ne = O.passes(got, ref, 1.0, 1.0, K)
+        assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
+
+
+def test_hipblaslt_comparator_agrees_with_oracle():
+    M, N, K = 512, 768, 256
+    Ab = O.lcg_fill_f16(M * K, 5)
+    Bb = O.lcg_fill_f16(K * N, 6)
+    A, B = _to_dev(Ab, (M, K)), _to_dev(Bb, (K, N))
+    ref = O.gemm_f64(Ab, Bb, M, N, K)
+    blas = G.BlasLt()
+    C16 = torch.empty((M, N), dtype=torch.float16, device=DEV)
+    C32 = torch.empty((M, N), dtype=torch.float32, device=DEV)
+    blas.gemm(A, B, C16, M, N, K)
+    blas.gemm(A, B, C32, M, N, K, c_is_f32=True)
+    torch.cuda.synchronize()
+    assert O.passes(O.f16_bits_to_f32(_bits(C16)), ref, 0.5, 0.5, K)[0]
+    assert O.passes(C32.cpu().numpy(), ref, 0.5, 0.5, K)[0]
+    blas.close()
