@@ -1,0 +1,227 @@
+#!/usr/bin/env python3
+"""Headline benchmark: FP16 GEMM TFLOP/s at 4096^3 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant BM,BN,BK,WM,WN,S,G]
+                    [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt]
+    python bench.py --mode copy     # plain device copy of known size, for scaling
+                                    # rocprofv3 FETCH_SIZE / WRITE_SIZE counters
+
+A step is one C = A * B launch (FP16 A, B row-major from a seeded U[-1,1) device
+fill, FP32 accumulate, FP16 C) through the C ABI, with inputs resident in HBM
+before the timed region. W untimed steps, then exactly K timed steps bracketed by
+torch.cuda.synchronize(); value = 2 M N K K / elapsed. The same launches are also
+bracketed by HIP events on the launch stream for the roofline figure, and the
+hipBLASLt comparator (best of its heuristic candidates, best of a before and an
+after reading, as the reference does in bench/check-gemm.cu:357-391) is timed the
+same way. Prints ONE JSON line.
+
+cpu_baseline: the CPU f64 GEMM of the oracle (a port of the reference's CPU
+reference, bench/check-gemm.cu:98-108, row-parallel with OpenMP) timed on a
+bounded sample of the same 4096^3 workload (a block of output rows, about 10 s of
+work), reported in TFLOP/s with the thread count used.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+# Datasheet dense FP16 MFMA peak of MI355X: 256 CUs x 4096 FLOP/clk/CU x 2.4 GHz.
+PEAK_FP16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+DEFAULT_SHAPE = (4096, 4096, 4096)
+# The registered variant the sweep measured fastest at 4096^3.
+DEFAULT_VARIANT = (256, 256, 64, 128, 64, 2, 8)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_4096_traffic.json")
+
+
+def parse_ints(s, n):
+    v = tuple(int(x) for x in s.split(","))
+    if len(v) != n:
+        raise SystemExit("expected %d comma-separated integers, got %r" % (n, s))
+    return v
+
+
+def time_launches(fn, steps, stream):
+    """Wall time of `steps` calls bracketed by synchronize, and the HIP-event time
+    of the same calls on the launch stream. Returns (wall_s, event_ms)."""
+    import torch
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, e0.elapsed_time(e1)
+
+
+def cpu_baseline(M, N, K, seconds=10.0):
+    """f64 oracle GEMM on a block of output rows of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    Ab = O.uniform_fill_f16(M * K, 1).reshape(M, K)
+    Bb = O.uniform_fill_f16(K * N, 2)
+    threads = os.cpu_count() or 1
+    # Grow the row block until one call takes about `seconds` (each call also
+    # pays the one-off conversion of B, which the first small blocks are
+    # dominated by, so the estimate is refined from the previous call).
+    rows = 16
+    while True:
+        t0 = time.perf_counter()
+        O.gemm_f64(Ab[:rows].ravel(), Bb, rows, N, K, threads=threads)
+        dt = time.perf_counter() - t0
+        if dt >= 0.5 * seconds or rows >= M:
+            break
+        rows = int(min(M, max(2 * rows, rows * seconds / max(dt, 1e-3))))
+    tflops = 2.0 * rows * N * K / dt / 1e12
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": "%d of %d output rows of %dx%dx%d (f64 accumulate, %.1f s)" % (rows, M, M, N, K, dt)}
+
+
+def run_copy_mode(steps):
+    """A plain device-to-device copy of known size, the scaling reference for the
+    rocprofv3 FETCH_SIZE and WRITE_SIZE counters."""
+    import torch
+    nbytes = 256 << 20
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda:0")
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "copy", "bytes_per_copy": nbytes, "copies": steps}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--variant", default=",".join(str(x) for x in DEFAULT_VARIANT))
+    ap.add_argument("--shape", default=",".join(str(x) for x in DEFAULT_SHAPE))
+    ap.add_argument("--warm-seconds", type=float, default=3.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-blaslt", action="store_true")
+    ap.add_argument("--mode", default="gemm", choices=["gemm", "copy"])
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMM is "
+              "single-device by design; see the sharding notes). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    if args.mode == "copy":
+        run_copy_mode(max(args.steps, 1))
+        return
+
+    from ridge_amd import gemm as G
+
+    M, N, K = parse_ints(args.shape, 3)
+    key = parse_ints(args.variant, 7)
+    idx = G.find_variant(*key)
+    if idx < 0:
+        raise SystemExit("variant %s is not in the registered table" % (key,))
+    v = G.variant(idx)
+    if not v.divides(M, N, K):
+        raise SystemExit("variant %s does not divide %dx%dx%d" % (v.label(), M, N, K))
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    A = torch.empty((M, K), dtype=torch.float16, device=dev)
+    B = torch.empty((K, N), dtype=torch.float16, device=dev)
+    C = torch.empty((M, N), dtype=torch.float16, device=dev)
+    G.fill_uniform(A, 1)
+    G.fill_uniform(B, 2)
+    torch.cuda.synchronize()
+    flops = 2.0 * M * N * K
+
+    def step():
+        rc = G.launch(idx, A, B, C, M, N, K, stream)
+        if rc != 0:
+            raise SystemExit("ridge_gemm_launch returned %d" % rc)
+
+    # Clock ramp: a few seconds of the same work before anything is timed
+    # (the reference warms 5 s, check-gemm.cu:41-45).
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < args.warm_seconds:
+        for _ in range(50):
+            step()
+        torch.cuda.synchronize()
+
+    blas = None
+    blas_before = blas_after = None
+    if not args.no_blaslt:
+        blas = G.BlasLt()
+        blas.prepare(A, B, C, M, N, K, candidates=16, iters=20, stream=stream)
+
+        def blas_step():
+            blas.gemm(A, B, C, M, N, K, stream=stream)
+
+        for _ in range(args.warmup):
+            blas_step()
+        _, ms = time_launches(blas_step, args.steps, stream)
+        blas_before = flops * args.steps / (ms * 1e-3) / 1e12
+
+    for _ in range(args.warmup):
+        step()
+    wall, ev_ms = time_launches(step, args.steps, stream)
+    value = flops * args.steps / wall / 1e12
+    per_launch_ms = ev_ms / args.steps
+    achieved = flops / (per_launch_ms * 1e-3) / 1e12
+
+    if blas is not None:
+        _, ms = time_launches(blas_step, args.steps, stream)
+        blas_after = flops * args.steps / (ms * 1e-3) / 1e12
+        blas.close()
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        if tuple(t.get("shape", ())) == (M, N, K) and tuple(t.get("variant", ())) == key:
+            traffic = t.get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": "FP16 GEMM TFLOP/s @4096^3 on 1 MI355X (% MFMA peak, % hipBLASLt); top-10 regret",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: A, B ~ U[-1,1) FP16 from splitmix64 seeds 1 and 2, generated on the device",
+        "config": {"workload": "FP16 GEMM M=%d N=%d K=%d, row-major A/B/C, FP32 accumulate, FP16 C" % (M, N, K),
+                   "variant": v.label(), "parallelism": "single GPU"},
+        "frac_of_mfma_peak": round(value / PEAK_FP16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic},
+    }
+    if blas_before is not None:
+        best = max(blas_before, blas_after)
+        out["hipblaslt"] = {"tflops": round(best, 3), "before": round(blas_before, 3),
+                            "after": round(blas_after, 3),
+                            "drift": round(abs(blas_after - blas_before) / blas_before, 4),
+                            "frac_of_hipblaslt": round(value / best, 4)}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(M, N, K)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -49,6 +49,11 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 #define RIDGE_LDS_AS __attribute__((address_space(3)))
 
+// 1: order each k-step's MFMAs and LDS reads with sched_group_barrier hints.
+#ifndef RIDGE_GEMM_SCHED
+#define RIDGE_GEMM_SCHED 1
+#endif
+
 constexpr int kWaveSize = 64;
 constexpr int kXcds = 8;
 // MFMA instruction shape (v_mfma_f32_32x32x16_f16): 32768 FLOP per instruction.
@@ -138,11 +143,12 @@ struct GemmTraits {
     static_assert(BM % WM == 0 && BN % WN == 0, "workgroup tile must split into wave tiles");
     static_assert(WM % kMfmaM == 0 && WN % kMfmaN == 0, "wave tile must split into 32x32 MFMA tiles");
     static_assert(BK % kMfmaK == 0, "BK must be a whole number of MFMA k-steps");
+    static_assert(kSteps % 2 == 0, "fragment double-buffering assumes an even number of k-steps");
     static_assert(BK == 32 || BK == 64, "the A swizzle is derived for BK of 32 or 64");
     static_assert(BN == 64 || BN == 128 || BN == 256, "the B swizzle is derived for BN of 64, 128 or 256");
     static_assert(kBytesA % 1024 == 0 && kBytesB % 1024 == 0, "tiles must be whole 1 KiB wave loads");
     static_assert(kInstA % kWaves == 0 && kInstB % kWaves == 0, "loads must split evenly over waves");
-    static_assert((STAGES - 2) * kLoadsPerTile < 64, "in-flight loads exceed the vmcnt counter");
+    static_assert((STAGES - 1) * kLoadsPerTile < 64, "in-flight loads exceed the vmcnt counter");
     static_assert(kLdsBytes <= 163840, "LDS is 160 KiB per workgroup on gfx950");
 };
 
@@ -179,7 +185,8 @@ void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__
 
     // Per-lane global element offsets of this wave's direct-to-LDS loads,
     // relative to the tile origin. Wave instruction j fills physical chunks
-    // [64 j, 64 j + 64); lane t's chunk holds logical chunk swizzle(64 j + t).
+    // [64 j, 64 j + 64) of a stage; lane t's chunk holds logical chunk
+    // swizzle(64 j + t).
     int offA[T::kPerWaveA];
     int offB[T::kPerWaveB];
 #pragma unroll
@@ -253,60 +260,96 @@ void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__
 
     const int numK = K / BK;
 
-    // Prologue: tiles 0 .. STAGES-2 in flight. A tile that does not exist is
-    // simply not issued; the waits below count only issued loads.
+    // Operand fragments of one k-step: TM A reads (ds_read_b128) and 2 TN
+    // transposing B reads.
+    auto readFrags = [&](const char* base, int ks, half8_t (&a)[TM], half8_t (&b)[TN]) {
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) {
+        for (int tm = 0; tm < TM; ++tm) {
+            a[tm] = *(const RIDGE_LDS_AS half8_t*)(base + rdA[tm][ks]);
+        }
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            const char* p = base + rdB[tn] + ks * 16 * CPR_B * 16;
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RIDGE_LDS_AS short4_t*)(p));
+            const short4_t hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((RIDGE_LDS_AS short4_t*)(p + 4 * CPR_B * 16));
+            const half4_t l4 = __builtin_bit_cast(half4_t, lo);
+            const half4_t h4 = __builtin_bit_cast(half4_t, hi);
+            b[tn] = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+        }
+    };
+    auto mfmaStep = [&](const half8_t (&a)[TM], const half8_t (&b)[TN]) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+                acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
+    };
+    // Scheduling hint for one k-step: alternate one MFMA with one LDS read so
+    // the reads of the next k-step hide under this step's matrix work.
+    auto interleave = [&]() {
+#if RIDGE_GEMM_SCHED
+        constexpr int kMfmas = TM * TN;
+        constexpr int kReads = TM + 2 * TN;
+#pragma unroll
+        for (int i = 0; i < kMfmas; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if (kReads > kMfmas) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kMfmas, 0);
+#endif
+    };
+
+    // Prologue: every stage filled (tiles 0 .. STAGES-1). A tile that does not
+    // exist is not issued; the waits count only issued loads, and near the end of
+    // K fewer were issued, so those waits drain fully.
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
         if (s < numK) issueTile(s, s);
     }
+    if (numK >= STAGES) {
+        waitVmcnt<(STAGES - 1) * T::kLoadsPerTile>();
+    } else {
+        waitVmcnt<0>();
+    }
+    barrierLds();
 
+    half8_t fa[2][TM];
+    half8_t fb[2][TN];
+    readFrags(lds, 0, fa[0], fb[0]);
+
+    // Fragments are double-buffered across k-steps (kSteps is even, so the
+    // buffer parity is the same in every K tile). The tile boundary sits inside
+    // the last k-step: once tile kt+1 has landed and every wave is past its reads
+    // of tile kt, the freed stage is refilled with tile kt+STAGES and the first
+    // fragments of tile kt+1 are read while the last MFMAs of tile kt run.
     int stage = 0;
     for (int kt = 0; kt < numK; ++kt) {
-        // Tile kt has landed once at most the loads of tiles kt+1 .. kt+STAGES-2
-        // are outstanding. Near the end fewer were issued, so drain fully.
-        if (kt + STAGES - 2 < numK) {
-            waitVmcnt<(STAGES - 2) * T::kLoadsPerTile>();
-        } else {
-            waitVmcnt<0>();
-        }
-        // Every wave's share of tile kt is in LDS, and every wave has finished
-        // reading tile kt-1, whose buffer the prefetch below overwrites.
-        barrierLds();
-
-        const int nextTile = kt + STAGES - 1;
-        if (nextTile < numK) {
-            int nextStage = stage + STAGES - 1;
-            if (nextStage >= STAGES) nextStage -= STAGES;
-            issueTile(nextTile, nextStage);
-        }
-
         const char* base = lds + stage * T::kStageBytes;
+        const int nextStage = (stage + 1 == STAGES) ? 0 : stage + 1;
 #pragma unroll
         for (int ks = 0; ks < T::kSteps; ++ks) {
-            half8_t a[TM];
-            half8_t b[TN];
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm) {
-                a[tm] = *(const RIDGE_LDS_AS half8_t*)(base + rdA[tm][ks]);
+            const int cur = ks & 1;
+            if (ks + 1 < T::kSteps) {
+                readFrags(base, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            } else if (kt + 1 < numK) {
+                // Tile kt+1 has landed once at most tiles kt+2 .. kt+STAGES-1 are
+                // outstanding.
+                if (kt + STAGES - 1 < numK) {
+                    waitVmcnt<(STAGES - 2) * T::kLoadsPerTile>();
+                } else {
+                    waitVmcnt<0>();
+                }
+                // This wave's reads of tile kt completed (lgkmcnt(0)) and every
+                // wave arrived, so stage `stage` is free and tile kt+1 is visible.
+                barrierLds();
+                if (kt + STAGES < numK) issueTile(kt + STAGES, stage);
+                readFrags(lds + nextStage * T::kStageBytes, 0, fa[cur ^ 1], fb[cur ^ 1]);
             }
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                const char* p = base + rdB[tn] + ks * 16 * CPR_B * 16;
-                const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RIDGE_LDS_AS short4_t*)(p));
-                const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (RIDGE_LDS_AS short4_t*)(p + 4 * CPR_B * 16));
-                const half4_t l4 = __builtin_bit_cast(half4_t, lo);
-                const half4_t h4 = __builtin_bit_cast(half4_t, hi);
-                b[tn] = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-            }
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
-                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
+            mfmaStep(fa[cur], fb[cur]);
+            interleave();
         }
-
-        stage = (stage + 1 == STAGES) ? 0 : stage + 1;
+        stage = nextStage;
     }
 
     // Epilogue: FP32 -> FP16 (round to nearest even) and 8-byte stores of four
@@ -328,6 +371,9 @@ void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__
                 v[3] = (_Float16)acc[tm][tn][4 * i + 3];
                 *(half4_t*)(crow + n0 + 8 * i) = v;
             }
+            // One tile at a time: without this fence the scheduler hoists every
+            // accumulator read to the top of the epilogue and runs out of VGPRs.
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }

@@ -57,7 +57,7 @@ def test_no_variant_spills():
 
 
 def test_divisibility_and_bad_launches_are_rejected_before_any_gpu_call():
-    i = G.find_variant(256, 256, 64, 128, 128, 2, 8)
+    i = G.find_variant(256, 256, 64, 128, 64, 2, 8)
     v = G.variant(i)
     assert v.divides(4096, 4096, 4096)
     assert not v.divides(4096, 4096, 4000)
