@@ -1,0 +1,63 @@
+// ridge/hardware.h -- per-GPU constants of the cost model.
+//
+// The ten required keys and their meaning follow the reference's HardwareModel
+// (include/ridge/hardware.h:9-54): constants marked [CAL] come from the
+// calibration microbenchmarks, the rest from the datasheet. "SM" fields mean a
+// compute unit (CU) on CDNA, "warp" fields a 64-lane wavefront.
+//
+// The target-description fields below the required keys capture every place the
+// reference hard-codes an sm_80 assumption. Their defaults ARE those assumptions,
+// so a model built from a reference JSON (or a100()) predicts exactly what the
+// reference predicts; mi355x() and a calibrated gfx950 JSON switch them to CDNA4.
+#pragma once
+#include <string>
+
+namespace ridge {
+
+struct HardwareModel {
+    std::string name;
+    int numSMs = 0;                  // SMs (sm_80) or CUs (CDNA)
+    double clockHz = 0.0;
+
+    double mmaCyclesPerInst = 0.0;   // [CAL] SM/CU-level cycles per matrix instruction
+    double smemBytesPerCycle = 0.0;  // [CAL] operand-read bytes per cycle per SM/CU
+    double hbmBytesPerSec = 0.0;     // [CAL] sustained DRAM read bandwidth, whole GPU
+
+    int regsPerSM = 0;               // 32-bit registers per SM; lane-registers per CU on CDNA
+    int smemBytesPerSM = 0;          // shared memory / LDS per SM/CU
+    int maxWarpsPerSM = 0;           // resident warps / wavefronts per SM/CU
+    int maxCtasPerSM = 0;            // resident workgroups per SM/CU
+
+    double warpsNeededToHide = 0.0;  // [CAL] resident warps/waves that hide latency
+
+    bool calibrated = false;         // every [CAL] constant came from a measurement
+
+    // ---- target description (defaults = the reference's sm_80 assumptions) ----
+    std::string arch = "sm_80";
+    int waveSize = 32;               // threads per warp / lanes per wavefront
+    int mmaM = 16, mmaN = 8, mmaK = 16;  // matrix instruction shape (FP16)
+    int simdsPerSM = 0;              // 0: pooled register file (sm_80 accounting);
+                                     // >0: per-SIMD files, waves spread over SIMDs
+    int regsPerSimdLane = 0;         // VGPR+AGPR budget per lane per SIMD (512 on CDNA3/4)
+    int regGranule = 1;              // per-lane register allocation granule (8 on gfx950)
+    int numXcds = 1;                 // separate L2 domains (8 XCDs on MI355X)
+    int cBytes = 4;                  // bytes per output element drained by the epilogue
+    int l2ReuseModel = 0;            // 0: sqrt(ctaSlots) square reuse (reference)
+                                     // 1: per-XCD resident block, bounded by the grid
+
+    // Datasheet placeholders of the reference (hardware.cpp:19-34).
+    static HardwareModel a100();
+
+    // MI355X (gfx950) datasheet placeholders; calibration replaces the [CAL] ones.
+    static HardwareModel mi355x();
+
+    // All-or-nothing load of a flat JSON written by the calibration driver (or the
+    // reference's data/hardware/*.json). The ten required keys must be present and
+    // the [CAL] ones positive; "arch": "gfx950" selects the CDNA4 target
+    // description, and any target-description key present overrides it. On
+    // failure returns false, leaves `out` untouched and sets `err`
+    // (reference hardware.h:38-48).
+    static bool loadFromJson(const std::string& path, HardwareModel& out, std::string& err);
+};
+
+}  // namespace ridge

@@ -1,0 +1,53 @@
+// ridge/prediction.h -- the cost model's output.
+//
+// Same labels and fields as the reference (include/ridge/prediction.h:10-49),
+// plus the CDNA4 terms (XCD-aware reuse) that explain the new HBM branch.
+#pragma once
+
+namespace ridge {
+
+// TENSOR_CORE: the matrix pipe binds; SMEM: operand reads from LDS/shared memory
+// serialise with the math; HBM: the memory roofline binds; OCC: too few resident
+// waves to hide latency; WAVES: the grid does not fill the machine; ENVELOPE:
+// pipeline fill and drain dominate; DOES_NOT_FIT: the tile exceeds a CU/SM.
+enum class Bottleneck { TensorCore, Smem, Hbm, Occupancy, Waves, Envelope, DoesNotFit };
+
+const char* toString(Bottleneck b);
+
+struct Prediction {
+    double predictedTFLOPS = 0.0;
+    Bottleneck bottleneck = Bottleneck::TensorCore;
+
+    double computeTFLOPS = 0.0;        // compute ceiling after all deratings
+    double hbmTFLOPS = 0.0;            // HBM roofline ceiling
+    double peakTensorTFLOPS = 0.0;     // matrix-pipe peak, no derating
+    double smEfficiency = 0.0;         // tCompute / tStep
+    double occFactor = 0.0;            // latency hiding, 1.0 = fully hidden
+    double arithmeticIntensity = 0.0;  // FLOP per DRAM byte, after cache reuse
+    double baseIntensity = 0.0;        // FLOP per byte of one tile, before reuse
+    double l2ReuseFactor = 0.0;        // arithmeticIntensity / baseIntensity
+
+    double waveEfficiency = 0.0;       // busy fraction from grid quantisation
+    double totalCtas = 0.0;
+    double ctaSlots = 0.0;             // resident workgroups per CU * CUs
+    double wavesExact = 0.0;           // totalCtas / ctaSlots
+
+    double envelopeEfficiency = 0.0;   // steady-state fraction of the kernel
+    double tPrologueCycles = 0.0;
+    double tEpilogueCycles = 0.0;
+    double tBodyCycles = 0.0;
+    double kSteps = 0.0;
+
+    int numWarps = 0;                  // waves (warps) per workgroup
+    int ctasPerSM = 0;                 // resident workgroups per CU (SM)
+    double tComputeCycles = 0.0;
+    double tSmemCycles = 0.0;
+    double tStepCycles = 0.0;          // tCompute + tSmem, in series
+
+    // CDNA4 reuse terms (zero in the reference's square-reuse mode).
+    double reuseTilesM = 0.0;          // resident row tiles sharing one XCD's L2
+    double reuseTilesN = 0.0;          // resident column tiles sharing it
+    double compulsoryIntensity = 0.0;  // 2MNK / (A + B + C bytes)
+};
+
+}  // namespace ridge

@@ -1,0 +1,222 @@
+// model.cpp -- the closed-form GEMM cost model.
+//
+// Counterpart of the reference's src/model.cpp:22-146 and src/mma.cpp:5-12. The
+// structure of the reference model is kept term for term (per-step compute and
+// operand-read time in series, occupancy, wave quantisation, fill/drain
+// envelope, HBM roofline, worst-factor label), and every sm_80 assumption it
+// hard-codes is read from the hardware model instead:
+//
+//   threads per workgroup = waves * hw.waveSize             (reference :31, *32)
+//   matrix instruction    = hw.mmaM x mmaN x mmaK           (reference mma.cpp:9)
+//   register occupancy    = per-SIMD files when hw.simdsPerSM > 0: a workgroup's
+//                           waves spread over the SIMDs, each lane holds its
+//                           VGPR+AGPR count rounded to hw.regGranule
+//   epilogue drain        = BM * BN * hw.cBytes              (reference :99, * 4)
+//   L2 reuse              = hw.l2ReuseModel 1: the workgroups resident on one
+//                           XCD form a compact block of output tiles, bounded by
+//                           the grid, and fetch their A and B panels once into
+//                           that XCD's L2; capped by the compulsory intensity of
+//                           the whole problem                 (reference :116-123)
+//
+// With the defaults (a100() or a reference JSON) every term reduces to the
+// reference's expression in the same double-precision operation order, so the
+// A100 predictions match the reference bit for bit; integer divisions are kept
+// where the reference has them.
+
+#include "ridge/mma.h"
+#include "ridge/model.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace ridge {
+
+const char* toString(Bottleneck b) {
+    switch (b) {
+        case Bottleneck::TensorCore: return "TENSOR_CORE";
+        case Bottleneck::Smem: return "SMEM";
+        case Bottleneck::Hbm: return "HBM";
+        case Bottleneck::Occupancy: return "OCC";
+        case Bottleneck::Waves: return "WAVES";
+        case Bottleneck::Envelope: return "ENVELOPE";
+        case Bottleneck::DoesNotFit: return "DOES_NOT_FIT";
+    }
+    return "UNKNOWN";
+}
+
+MmaShape mmaShapeFor(DType dtype) {
+    switch (dtype) {
+        case DType::FP16: return MmaShape{16, 8, 16, 2LL * 16 * 8 * 16};
+    }
+    return MmaShape{16, 8, 16, 2LL * 16 * 8 * 16};
+}
+
+MmaShape mmaShapeFor(DType dtype, const HardwareModel& hw) {
+    (void)dtype;  // FP16 is the only dtype
+    return MmaShape{hw.mmaM, hw.mmaN, hw.mmaK, 2LL * hw.mmaM * hw.mmaN * hw.mmaK};
+}
+
+namespace {
+
+// Workgroups per CU allowed by the register file.
+double workgroupsByRegisters(const GemmConfig& cfg, const HardwareModel& hw, int numWarps, int threadsPerCta) {
+    if (cfg.regsPerThread <= 0) return 1e9;
+    if (hw.simdsPerSM <= 0) {
+        // One pooled file per SM (reference :59-62).
+        return std::floor(double(hw.regsPerSM) / (double(cfg.regsPerThread) * threadsPerCta));
+    }
+    // Per-SIMD files: each wave of the workgroup lands on one SIMD, and a SIMD
+    // holds floor(budget / rounded-registers) waves.
+    const int g = hw.regGranule;
+    const int rounded = (cfg.regsPerThread + g - 1) / g * g;
+    const double wavesPerSimd = std::floor(double(hw.regsPerSimdLane) / rounded);
+    const double wavesPerSimdPerCta = std::ceil(double(numWarps) / hw.simdsPerSM);
+    return std::floor(wavesPerSimd / wavesPerSimdPerCta);
+}
+
+}  // namespace
+
+Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
+    GemmConfig cfg = cfgIn;
+    const MmaShape mma = mmaShapeFor(cfg.dtype, hw);
+    if (cfg.mmaM == 0) {
+        cfg.mmaM = mma.m;
+        cfg.mmaN = mma.n;
+        cfg.mmaK = mma.k;
+    }
+    const int db = dtypeBytes(cfg.dtype);
+
+    Prediction p;
+
+    const int numWarps = (cfg.BM / cfg.warpM) * (cfg.BN / cfg.warpN);
+    const int threadsPerCta = numWarps * hw.waveSize;
+    p.numWarps = numWarps;
+
+    // Per K-step times of one workgroup: matrix instructions, and the operand
+    // reads out of LDS that feed them (in series: the next instruction consumes
+    // the registers the read just wrote). The global->LDS copies are
+    // asynchronous and appear only in the envelope.
+    const double mmasPerWarpPerStep =
+        double(cfg.warpM / cfg.mmaM) * (cfg.warpN / cfg.mmaN) * (cfg.BK / cfg.mmaK);
+    const double tCompute = mmasPerWarpPerStep * numWarps * hw.mmaCyclesPerInst;
+    const double smemBytesPerStep = double(numWarps) * (cfg.warpM + cfg.warpN) * cfg.BK * db;
+    const double tSmem = smemBytesPerStep / hw.smemBytesPerCycle;
+    const double tStep = tCompute + tSmem;
+    const double smEfficiency = tCompute / tStep;
+    p.tComputeCycles = tCompute;
+    p.tSmemCycles = tSmem;
+    p.tStepCycles = tStep;
+    p.smEfficiency = smEfficiency;
+
+    // Occupancy: the tightest of LDS, wave slots, registers and the workgroup cap.
+    const double smemBytesPerCta = double(cfg.stages) * (cfg.BM * cfg.BK + cfg.BK * cfg.BN) * db;
+    const double ctasBySmem = std::floor(hw.smemBytesPerSM / smemBytesPerCta);
+    const double ctasByWarps = std::floor(double(hw.maxWarpsPerSM) / numWarps);
+    const double ctasByRegs = workgroupsByRegisters(cfg, hw, numWarps, threadsPerCta);
+    const double ctasPerSM =
+        std::min(std::min(ctasBySmem, ctasByWarps), std::min(ctasByRegs, double(hw.maxCtasPerSM)));
+    if (ctasPerSM < 1.0) {
+        p.bottleneck = Bottleneck::DoesNotFit;
+        p.ctasPerSM = 0;
+        return p;
+    }
+    p.ctasPerSM = int(ctasPerSM);
+
+    const double activeWarps = ctasPerSM * numWarps;
+    const double occFactor = std::min(1.0, activeWarps / hw.warpsNeededToHide);
+    p.occFactor = occFactor;
+
+    // Wave quantisation over all resident workgroup slots.
+    const double ctaSlots = ctasPerSM * double(hw.numSMs);
+    const double totalCtas = double((cfg.M / cfg.BM) * (cfg.N / cfg.BN));
+    const double wavesExact = totalCtas / ctaSlots;
+    const double fullWaves = std::ceil(wavesExact);
+    const double waveEfficiency = fullWaves > 0.0 ? totalCtas / (fullWaves * ctaSlots) : 1.0;
+    p.ctaSlots = ctaSlots;
+    p.totalCtas = totalCtas;
+    p.wavesExact = wavesExact;
+    p.waveEfficiency = waveEfficiency;
+
+    // Fill and drain: STAGES-1 tiles land before the first instruction, the output
+    // tile drains after the last; only the first fill and last drain of a CU are
+    // exposed, hence the division by resident workgroups.
+    const double gmemBytesPerCycle = hw.hbmBytesPerSec / (hw.clockHz * double(hw.numSMs));
+    const double tileBytes = double(cfg.BM * cfg.BK + cfg.BK * cfg.BN) * db;
+    const double kSteps = double(cfg.K) / cfg.BK;
+    const double tPrologue = double(cfg.stages - 1) * tileBytes / gmemBytesPerCycle / ctasPerSM;
+    const double tEpilogue = double(cfg.BM) * cfg.BN * double(hw.cBytes) / gmemBytesPerCycle / ctasPerSM;
+    const double tBody = kSteps * tStep;
+    const double envelopeEfficiency = tBody / (tPrologue + tBody + tEpilogue);
+    p.kSteps = kSteps;
+    p.tPrologueCycles = tPrologue;
+    p.tEpilogueCycles = tEpilogue;
+    p.tBodyCycles = tBody;
+    p.envelopeEfficiency = envelopeEfficiency;
+
+    // Compute ceiling: resident workgroups share the matrix pipes, so occupancy
+    // hides latency but never multiplies the peak.
+    const double peakTensorTFLOPS = (double(mma.flops) / hw.mmaCyclesPerInst) * hw.clockHz * hw.numSMs / 1e12;
+    const double computeTFLOPS = peakTensorTFLOPS * smEfficiency * occFactor * waveEfficiency * envelopeEfficiency;
+    p.peakTensorTFLOPS = peakTensorTFLOPS;
+    p.computeTFLOPS = computeTFLOPS;
+
+    // HBM roofline.
+    const double globalBytesPerCta = double(cfg.BM * cfg.K + cfg.K * cfg.BN) * db;
+    const double flopsPerCta = 2.0 * double(cfg.BM) * cfg.BN * cfg.K;
+    const double baseIntensity = flopsPerCta / globalBytesPerCta;
+    double arithmeticIntensity;
+    if (hw.l2ReuseModel == 0) {
+        // Square reuse over all resident slots (reference :116-123).
+        const double l2ReuseFactor = std::sqrt(ctaSlots);
+        arithmeticIntensity = baseIntensity * l2ReuseFactor;
+        p.l2ReuseFactor = l2ReuseFactor;
+    } else {
+        // The workgroups resident on one XCD at a time, as compact a block of
+        // output tiles as the grid allows: a rows x b columns of tiles. Each XCD
+        // fetches a row panels of A and b column panels of B once into its own
+        // L2. The block can never exceed the grid, which is what lets a
+        // tall-skinny problem (one column of tiles) reach the HBM branch.
+        const double numPidM = double(cfg.M / cfg.BM);
+        const double numPidN = double(cfg.N / cfg.BN);
+        const double perXcd = std::max(1.0, std::min(ctaSlots, totalCtas) / double(hw.numXcds));
+        double a = std::max(1.0, std::min(numPidM, std::floor(std::sqrt(perXcd))));
+        const double b = std::max(1.0, std::min(numPidN, std::ceil(perXcd / a)));
+        a = std::max(1.0, std::min(numPidM, std::ceil(perXcd / b)));
+        const double blockFlops = 2.0 * (a * cfg.BM) * (b * cfg.BN) * double(cfg.K);
+        const double blockBytes = (a * cfg.BM + b * cfg.BN) * double(cfg.K) * db;
+        const double l2Intensity = blockFlops / blockBytes;
+        // No schedule beats the compulsory traffic of the whole problem.
+        const double M = double(cfg.M), N = double(cfg.N), K = double(cfg.K);
+        const double compulsory = 2.0 * M * N * K / ((M * K + K * N) * db + M * N * hw.cBytes);
+        arithmeticIntensity = std::min(l2Intensity, compulsory);
+        p.l2ReuseFactor = arithmeticIntensity / baseIntensity;
+        p.reuseTilesM = a;
+        p.reuseTilesN = b;
+        p.compulsoryIntensity = compulsory;
+    }
+    p.baseIntensity = baseIntensity;
+    p.arithmeticIntensity = arithmeticIntensity;
+    p.hbmTFLOPS = hw.hbmBytesPerSec * arithmeticIntensity / 1e12;
+
+    // The label names the derating furthest from 1.0 (reference :129-143).
+    p.predictedTFLOPS = std::min(computeTFLOPS, p.hbmTFLOPS);
+    if (p.hbmTFLOPS < computeTFLOPS) {
+        p.bottleneck = Bottleneck::Hbm;
+    } else {
+        const double worst =
+            std::min(std::min(smEfficiency, occFactor), std::min(waveEfficiency, envelopeEfficiency));
+        if (worst >= 0.95)
+            p.bottleneck = Bottleneck::TensorCore;
+        else if (worst == waveEfficiency)
+            p.bottleneck = Bottleneck::Waves;
+        else if (worst == envelopeEfficiency)
+            p.bottleneck = Bottleneck::Envelope;
+        else if (worst == smEfficiency)
+            p.bottleneck = Bottleneck::Smem;
+        else
+            p.bottleneck = Bottleneck::Occupancy;
+    }
+    return p;
+}
+
+}  // namespace ridge

@@ -22,8 +22,10 @@ def _declared(header):
 def test_every_declared_symbol_is_exported(header):
     names = _declared(header)
     assert names, header
+    from ridge_amd import model as RM
     libs = {
         "ridge_gemm.h": G.LIB_PATH,
+        "ridge_model.h": RM.LIB_PATH,
     }
     path = libs.get(os.path.basename(header))
     if path is None:

@@ -1,0 +1,207 @@
+"""The cost model (no GPU).
+
+A100 mode: the reference's hand-derived worked example and invariants
+(test/test-model.cpp:47-181), and byte-identical batch output against the
+reference's own model build on the reference's 336-row sweep.
+CDNA4 mode: a hand-derived worked example in the same style; the test follows
+the derivation, never the code.
+"""
+import filecmp
+import math
+import os
+import subprocess
+
+import pytest
+
+from ridge_amd import model as RM
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLD = os.path.join(ROOT, "tests", "golden")
+
+
+@pytest.fixture(scope="module")
+def a100():
+    return RM.Hardware("a100")
+
+
+@pytest.fixture(scope="module")
+def mi355x():
+    return RM.Hardware("mi355x")
+
+
+def test_a100_worked_example(a100):
+    # test-model.cpp:47-101, values derived by hand there.
+    p = RM.predict(a100, M=4096, N=4096, K=4096, BM=128, BN=128, BK=32, warpM=64, warpN=64, stages=3,
+                   regsPerThread=128)
+    assert p["numWarps"] == 4
+    assert p["tComputeCycles"] == pytest.approx(512.0, abs=1e-6)
+    assert p["tSmemCycles"] == pytest.approx(256.0, abs=1e-6)
+    assert p["tStepCycles"] == pytest.approx(768.0, abs=1e-6)
+    assert p["smEfficiency"] == pytest.approx(512.0 / 768.0, abs=1e-9)
+    assert p["ctasPerSM"] == 3
+    assert p["occFactor"] == pytest.approx(0.75, abs=1e-9)
+    assert p["totalCtas"] == pytest.approx(1024.0)
+    assert p["ctaSlots"] == pytest.approx(324.0)
+    assert p["wavesExact"] == pytest.approx(1024.0 / 324.0, abs=1e-9)
+    assert p["waveEfficiency"] == pytest.approx(1024.0 / 1296.0, abs=1e-9)
+    assert p["kSteps"] == pytest.approx(128.0)
+    assert p["tPrologueCycles"] == pytest.approx(831.651840, abs=1e-4)
+    assert p["tEpilogueCycles"] == pytest.approx(1663.303680, abs=1e-4)
+    assert p["tBodyCycles"] == pytest.approx(98304.0, abs=1e-6)
+    assert p["envelopeEfficiency"] == pytest.approx(0.975248, abs=1e-6)
+    assert p["peakTensorTFLOPS"] == pytest.approx(311.869440, abs=1e-3)
+    assert p["computeTFLOPS"] == pytest.approx(120.158068, abs=1e-4)
+    assert p["baseIntensity"] == pytest.approx(64.0)
+    assert p["l2ReuseFactor"] == pytest.approx(18.0)
+    assert p["arithmeticIntensity"] == pytest.approx(1152.0)
+    assert p["hbmTFLOPS"] == pytest.approx(2304.0, abs=1e-6)
+    assert p["predictedTFLOPS"] == pytest.approx(120.158068, abs=1e-4)
+    assert p["bottleneck"] == "SMEM"
+
+
+def test_a100_sub_wave_grid(a100):
+    # test-model.cpp:103-124: 16 CTAs in 324 slots.
+    p = RM.predict(a100, M=512, N=512, K=4096, BM=128, BN=128, BK=32, warpM=64, warpN=64, stages=3,
+                   regsPerThread=128)
+    assert p["totalCtas"] == 16 and p["ctaSlots"] == 324
+    assert p["waveEfficiency"] == pytest.approx(16 / 324, abs=1e-9)
+    assert p["predictedTFLOPS"] == pytest.approx(7.509879, abs=1e-4)
+    assert p["bottleneck"] == "WAVES"
+
+
+def test_a100_invariants(a100):
+    # test-model.cpp:126-181.
+    assert 250 < RM.predict(a100)["peakTensorTFLOPS"] < 400
+    p = RM.predict(a100, M=8192, N=8192, K=8192)
+    assert 0 < p["predictedTFLOPS"] <= p["computeTFLOPS"] + 1e-6 and p["predictedTFLOPS"] <= p["hbmTFLOPS"] + 1e-6
+    assert 0 < p["occFactor"] <= 1 and 0 < p["envelopeEfficiency"] <= 1 and p["ctasPerSM"] >= 1
+    assert 0 < p["smEfficiency"] < 1
+    big = RM.predict(a100, BM=256, BN=256, warpM=64, warpN=64)
+    small = RM.predict(a100, BM=64, BN=64, warpM=64, warpN=64)
+    assert big["baseIntensity"] > small["baseIntensity"]
+    deep = dict(M=4096, N=4096, K=4096, BM=128, BN=128, BK=32, warpM=64, warpN=64, stages=3, regsPerThread=128)
+    pd = RM.predict(a100, **deep)
+    ps = RM.predict(a100, **dict(deep, K=128))
+    assert ps["envelopeEfficiency"] < pd["envelopeEfficiency"] and ps["kSteps"] < pd["kSteps"]
+    assert ps["bottleneck"] == "ENVELOPE"
+    assert RM.predict(a100, BM=512, BN=512, BK=128, stages=8)["bottleneck"] == "DOES_NOT_FIT"
+
+
+@pytest.mark.parametrize("hw,fixture", [
+    ("tests/golden/a100-sxm4-40gb.json", "a100_predictions_ref_calibrated.csv"),
+    ("a100", "a100_predictions_ref_placeholder.csv"),
+])
+def test_a100_batch_byte_identical_to_reference_model(tmp_path, hw, fixture):
+    """Same pred_* strings (6 significant digits) and hence the same ranking and
+    tie structure as the reference's own model on its 336-row sweep."""
+    out = tmp_path / "pred.csv"
+    RM.predict_batch(os.path.join(GOLD, "a100_measured.csv"), str(out),
+                     hw=os.path.join(ROOT, hw) if hw.endswith(".json") else hw)
+    assert filecmp.cmp(str(out), os.path.join(GOLD, fixture), shallow=False)
+    ref_bin = os.path.join(ROOT, "oracle", "_ref", "ridge-predict")
+    if os.path.exists(ref_bin):  # the live reference build, where it exists
+        live = tmp_path / "live.csv"
+        cmd = [ref_bin] + (["--hw", os.path.join(ROOT, hw)] if hw.endswith(".json") else ["--gpu", hw])
+        subprocess.run(cmd + ["--batch", os.path.join(GOLD, "a100_measured.csv"), "--out", str(live)],
+                       check=True, capture_output=True)
+        assert filecmp.cmp(str(out), str(live), shallow=False)
+
+
+def test_mi355x_worked_example(mi355x):
+    """4096^3, 256x256x64 tile, 128x64 wavefront tile, 2 stages, 214 registers, on
+    the MI355X placeholders. Derivation:
+
+      waves          (256/128) x (256/64) = 8, 512 workitems
+      MFMA/wave/step (128/32) x (64/32) x (64/16) = 32
+      tCompute       32 x 8 waves x 8 cycles = 2048
+      tSmem          8 x (128 + 64) x 64 x 2 B = 196608 B / 128 = 1536
+      tStep          3584, smEff 2048/3584 = 0.571429
+      LDS            2 x (256x64 + 64x256) x 2 = 131072 -> floor(163840/131072) = 1
+      wave slots     floor(32/8) = 4
+      registers      214 -> 216 (granule 8); floor(512/216) = 2 waves/SIMD;
+                     8 waves over 4 SIMDs = 2 per SIMD -> 1 workgroup
+      workgroups/CU  1, occ min(1, 8/8) = 1
+      grid           16 x 16 = 256 in 256 slots: waveEff 1
+      gmem B/cycle   8e12 / (2.4e9 x 256) = 13.0208333
+      prologue       1 x 65536 / 13.0208333 = 5033.1648
+      epilogue       256 x 256 x 2 / 13.0208333 = 10066.3296
+      body           64 K-steps x 3584 = 229376
+      envelope       229376 / 244475.4944 = 0.938237
+      peak           32768 / 8 x 2.4e9 x 256 = 2516.5824 TFLOP/s
+      compute        2516.5824 x 0.571429 x 0.938237 = 1349.22
+      base AI        2 x 256 x 256 x 4096 / ((256 + 256) x 4096 x 2) = 128
+      per-XCD block  32 slots per XCD: a = floor(sqrt 32) = 5, b = ceil(32/5) = 7,
+                     a = ceil(32/7) = 5; AI = (5x256)(7x256)/((5+7)x256) = 746.667
+      compulsory     2 x 4096^3 / (3 x 4096^2 x 2) = 1365.33; AI = 746.667
+      HBM            8e12 x 746.667 = 5973.33 TFLOP/s; label SMEM (0.571 worst)
+    """
+    p = RM.predict(mi355x, M=4096, N=4096, K=4096, BM=256, BN=256, BK=64, warpM=128, warpN=64, stages=2,
+                   regsPerThread=214)
+    assert p["numWarps"] == 8
+    assert p["tComputeCycles"] == pytest.approx(2048.0)
+    assert p["tSmemCycles"] == pytest.approx(1536.0)
+    assert p["smEfficiency"] == pytest.approx(2048 / 3584, abs=1e-9)
+    assert p["ctasPerSM"] == 1 and p["occFactor"] == pytest.approx(1.0)
+    assert p["ctaSlots"] == 256 and p["waveEfficiency"] == pytest.approx(1.0)
+    assert p["tPrologueCycles"] == pytest.approx(5033.1648, abs=1e-3)
+    assert p["tEpilogueCycles"] == pytest.approx(10066.3296, abs=1e-3)
+    assert p["envelopeEfficiency"] == pytest.approx(0.938237, abs=1e-6)
+    assert p["peakTensorTFLOPS"] == pytest.approx(2516.5824, abs=1e-6)
+    assert p["computeTFLOPS"] == pytest.approx(2516.5824 * (2048 / 3584) * (229376 / 244475.4944), abs=1e-6)
+    assert p["baseIntensity"] == pytest.approx(128.0)
+    assert (p["reuseTilesM"], p["reuseTilesN"]) == (5.0, 7.0)
+    assert p["arithmeticIntensity"] == pytest.approx(1280 * 1792 / 3072, abs=1e-9)
+    assert p["compulsoryIntensity"] == pytest.approx(2 * 4096 / 6, abs=1e-9)
+    assert p["hbmTFLOPS"] == pytest.approx(8 * 1280 * 1792 / 3072, abs=1e-6)
+    assert p["bottleneck"] == "SMEM"
+
+
+def test_mi355x_register_occupancy_per_simd(mi355x):
+    # 4 waves of 133+128 = 261 registers: 264 rounded, floor(512/264) = 1 wave per
+    # SIMD; 4 waves over 4 SIMDs = 1 per SIMD -> 1 workgroup. At 74 registers:
+    # floor(512/80) = 6 waves per SIMD -> 6 workgroups by registers, LDS (64 KiB
+    # at 2 stages of 128x128x64) allows 2.
+    p = RM.predict(mi355x, BM=256, BN=128, BK=64, warpM=128, warpN=64, stages=2, regsPerThread=261)
+    assert p["ctasPerSM"] == 1
+    p = RM.predict(mi355x, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=74)
+    assert p["ctasPerSM"] == 2
+    # 600 registers exceed the 512 budget: does not fit.
+    assert RM.predict(mi355x, regsPerThread=600)["bottleneck"] == "DOES_NOT_FIT"
+
+
+def test_mi355x_tall_skinny_reuse_bounded_by_grid(mi355x):
+    # N = 128 with BN = 128: one column of tiles, so every tile reads its own A
+    # panel; the per-XCD block is a x 1 and intensity cannot exceed the
+    # compulsory 2MNK / bytes = 125.1 FLOP/B (the reference's sqrt(slots) would
+    # claim ~1000+).
+    p = RM.predict(mi355x, M=16384, N=128, K=8192, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2,
+                   regsPerThread=74)
+    assert p["reuseTilesN"] == 1
+    comp = 2 * 16384 * 128 * 8192 / ((16384 * 8192 + 8192 * 128) * 2 + 16384 * 128 * 2)
+    assert p["compulsoryIntensity"] == pytest.approx(comp)
+    assert p["arithmeticIntensity"] <= comp + 1e-9
+    sq = RM.predict(RM.Hardware("a100"), M=16384, N=128, K=8192, BM=128, BN=128, BK=64, warpM=64, warpN=64,
+                    stages=2, regsPerThread=74)
+    assert sq["arithmeticIntensity"] > 5 * p["arithmeticIntensity"]
+
+
+def test_hardware_json_loader_is_all_or_nothing(tmp_path):
+    good = tmp_path / "g.json"
+    good.write_text('{"name": "x", "note": "mentions numSMs and clockHz in prose", "arch": "gfx950", '
+                    '"numSMs": 256, "clockHz": 2.1e9, "mmaCyclesPerInst": 9.5, "smemBytesPerCycle": 200, '
+                    '"hbmBytesPerSec": 6.5e12, "regsPerSM": 131072, "smemBytesPerSM": 163840, '
+                    '"maxWarpsPerSM": 32, "maxCtasPerSM": 32, "warpsNeededToHide": 8}')
+    hw = RM.Hardware(str(good))
+    assert hw.calibrated and hw.name == "x"
+    p = RM.predict(hw, BM=256, BN=256, BK=64, warpM=128, warpN=64, stages=2, regsPerThread=214)
+    assert p["numWarps"] == 8 and p["reuseTilesM"] > 0   # gfx950 target description
+    bad = tmp_path / "b.json"
+    bad.write_text(good.read_text().replace('"smemBytesPerCycle": 200, ', ''))
+    with pytest.raises(ValueError, match="smemBytesPerCycle"):
+        RM.Hardware(str(bad))
+    zero = tmp_path / "z.json"
+    zero.write_text(good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 0'))
+    with pytest.raises(ValueError, match="zero or negative"):
+        RM.Hardware(str(zero))
+    with pytest.raises(ValueError, match="cannot open"):
+        RM.Hardware(str(tmp_path / "missing.json"))
