@@ -1,0 +1,181 @@
+"""Runs the four calibration microbenchmarks and writes the hardware JSON.
+
+    python -m ridge_amd.calibrate [--binary-dir ridge_amd/bin] [--out data/hardware/mi355x.json] [--check]
+
+Counterpart of the reference's bench/calibrate/run-calibration.py:29-159. The
+constants come from the benchmarks; the datasheet figures below are independent
+cross-checks that catch a broken benchmark, never sources of a value. With
+--check nothing is written and the exit code says whether every constant is in
+band. A constant out of band, or a benchmark reporting unstable repeats, refuses
+the write.
+
+MI355X differences from the reference driver:
+  * clockHz is the loaded engine clock MEASURED by cal-mma (shader-clock cycles
+    against the constant 100 MHz counter), not a pinned constant, because this
+    machine's clocks cannot be locked;
+  * the compute band is checked on the peak implied at the nominal clock (what
+    the cycle count alone says), the loaded-clock figure is reported beside it;
+  * the JSON carries the CDNA4 target description ("arch": "gfx950") and the
+    extra measured keys (MALL bandwidth, LDS control and per-pattern rates).
+"""
+
+import argparse
+import json
+import os
+import re
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+
+# Public datasheet figures, cross-checks only.
+SPECS = {
+    "gfx950": dict(name="MI355X", peak_tflops=2516.6, hbm_bytes_per_sec=8.0e12, cus=256, clock_hz=2.4e9),
+}
+
+BENCHMARKS = ["cal-mma", "cal-smem-bw", "cal-hbm-bw", "cal-latency"]
+
+
+def detect_arch(text):
+    m = re.search(r"GPU:.*\((gfx[0-9a-f]+)", text)
+    return m.group(1) if m else None
+
+
+def parse_results(text):
+    out = {}
+    for line in text.splitlines():
+        m = re.match(r"CAL_RESULT\s+(\S+)\s+(\S+)", line)
+        if m:
+            out[m.group(1)] = float(m.group(2))
+    return out
+
+
+def run_benchmark(binary_dir, name):
+    path = os.path.join(binary_dir, name)
+    if not os.path.exists(path):
+        sys.exit("%s not found: build with `python -m ridge_amd.build`" % path)
+    print("--- %s %s" % (name, "-" * (60 - len(name))), flush=True)
+    proc = subprocess.run([path], capture_output=True, text=True)
+    sys.stdout.write(proc.stdout)
+    if proc.stderr:
+        sys.stderr.write(proc.stderr)
+    sys.stdout.flush()
+    return parse_results(proc.stdout), proc.stdout, proc.returncode
+
+
+def check(label, value, low, high, unit, note=""):
+    ok = low <= value <= high
+    print("  %-28s %12.4g %-12s band [%.4g, %.4g]  %s" % (label, value, unit, low, high,
+                                                           "ok" if ok else "OUT OF BAND"))
+    if note:
+        print("  %-28s %s" % ("", note))
+    return ok
+
+
+def band_check(res, spec):
+    """True when every constant sits in its sanity band."""
+    ok = True
+    ok &= check("impliedPeakTflopsNominal", res["impliedPeakTflopsNominalClock"], spec["peak_tflops"] * 0.85,
+                spec["peak_tflops"] * 1.05, "TFLOP/s", "cycle count alone, at the nominal clock: tight band")
+    ok &= check("clockHz", res["clockHz"] / 1e9, spec["clock_hz"] * 0.5 / 1e9, spec["clock_hz"] * 1.02 / 1e9,
+                "GHz", "loaded clock; below nominal under power limits is expected")
+    ok &= check("smemBytesPerCycle", res["smemBytesPerCycle"], 0.25 * res["ldsControlBytesPerCycle"],
+                1.05 * res["ldsControlBytesPerCycle"], "B/cycle/CU", "bounded by the conflict-free control")
+    ok &= check("hbmBytesPerSec", res["hbmBytesPerSec"] / 1e12, spec["hbm_bytes_per_sec"] * 0.60 / 1e12,
+                spec["hbm_bytes_per_sec"] * 1.02 / 1e12, "TB/s", "above spec would mean the MALL, not HBM")
+    ok &= check("warpsNeededToHide", res["warpsNeededToHide"], 1, 32, "waves/CU")
+    return ok
+
+
+def hardware_json(res, spec, arch):
+    return {
+        "name": spec["name"],
+        "arch": arch,
+        "note": ("measured by ridge_amd/calibrate.py on a %s; clockHz is the loaded clock measured by cal-mma "
+                 "(clocks are not pinned on this machine); LDS rate is the GEMM's own read mix" % arch),
+        "numSMs": spec["cus"],
+        "clockHz": res["clockHz"],
+        "mmaCyclesPerInst": res["mmaCyclesPerInst"],
+        "smemBytesPerCycle": res["smemBytesPerCycle"],
+        "hbmBytesPerSec": res["hbmBytesPerSec"],
+        "regsPerSM": 131072,
+        "smemBytesPerSM": 163840,
+        "maxWarpsPerSM": 32,
+        "maxCtasPerSM": 32,
+        "warpsNeededToHide": res["warpsNeededToHide"],
+        "waveSize": 64,
+        "mmaM": 32,
+        "mmaN": 32,
+        "mmaK": 16,
+        "simdsPerSM": 4,
+        "regsPerSimdLane": 512,
+        "regGranule": 8,
+        "numXcds": 8,
+        "cBytes": 2,
+        "l2ReuseModel": 1,
+        "nominalClockHz": res.get("nominalClockHz", spec["clock_hz"]),
+        "impliedPeakTflops": res["impliedPeakTflops"],
+        "mallBytesPerSec": res.get("mallBytesPerSec", 0.0),
+        "ldsControlBytesPerCycle": res["ldsControlBytesPerCycle"],
+        "ldsAReadBytesPerCycle": res.get("ldsAReadBytesPerCycle", 0.0),
+        "ldsBTrReadBytesPerCycle": res.get("ldsBTrReadBytesPerCycle", 0.0),
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--binary-dir", default=os.path.join(PKG, "bin"))
+    ap.add_argument("--out", default=os.path.join(ROOT, "data", "hardware", "mi355x.json"))
+    ap.add_argument("--check", action="store_true", help="band-check only, write nothing")
+    ap.add_argument("--log", default=None, help="also write the benchmarks' output here")
+    args = ap.parse_args(argv)
+
+    results, banner, failed = {}, "", False
+    for name in BENCHMARKS:
+        res, out, rc = run_benchmark(args.binary_dir, name)
+        results.update(res)
+        banner += out
+        if rc != 0:
+            print("  %s exited %d: its constants are unstable" % (name, rc))
+            failed = True
+        print()
+    if args.log:
+        with open(args.log, "w") as f:
+            f.write(banner)
+
+    arch = detect_arch(banner)
+    if arch is None:
+        sys.exit("could not detect the GPU from the benchmark output")
+    if arch not in SPECS:
+        sys.exit("no datasheet entry for %s: add one to SPECS rather than reusing another card's" % arch)
+    spec = SPECS[arch]
+    required = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
+                "smemBytesPerCycle", "ldsControlBytesPerCycle", "hbmBytesPerSec", "warpsNeededToHide"]
+    missing = [k for k in required if k not in results]
+    if missing:
+        sys.exit("benchmarks did not report: %s" % ", ".join(missing))
+
+    print("detected %s (%s); sanity bands against its datasheet:" % (spec["name"], arch))
+    ok = band_check(results, spec)
+    if failed:
+        ok = False
+        print("\n  at least one benchmark reported unstable repeats")
+    print()
+    if not ok:
+        print("a constant is out of band or unstable: fix the benchmark rather than widening the band or "
+              "importing a value from another GPU")
+        return 1
+    if args.check:
+        print("all constants in band; run without --check to write")
+        return 0
+    os.makedirs(os.path.dirname(args.out) or ".", exist_ok=True)
+    with open(args.out, "w") as f:
+        json.dump(hardware_json(results, spec, arch), f, indent=2)
+        f.write("\n")
+    print("wrote", args.out)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

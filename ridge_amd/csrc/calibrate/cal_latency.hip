@@ -1,0 +1,153 @@
+// cal_latency.hip -- warpsNeededToHide: resident wavefronts per CU at which an
+// LDS-read -> MFMA dependency chain stops losing throughput.
+//
+// Counterpart of the reference's bench/calibrate/cal-latency.cu:56-257. Each
+// iteration of each of Ilp independent chains reads an A fragment with
+// ds_read_b128 from the kernel's swizzled layout and feeds it straight into
+// v_mfma_f32_32x32x16_f16, so the read latency sits in front of the matrix
+// instruction. The whole waves x ILP surface is printed; the reported constant
+// is the ILP = 2 column's first wave count within 95% of that column's best,
+// as in the reference. Waves 16 with ILP 8 is omitted: its accumulators
+// (8 x 16 per lane) plus fragments exceed the 128 registers a lane may hold at
+// four waves per SIMD.
+#include "cal_common.hpp"
+#include "gemm_mfma.hpp"
+
+using namespace ridgecal;
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kIters = 1000;
+constexpr double kSaturation = 0.95;
+
+template <int Waves, int Ilp>
+__global__ __launch_bounds__(Waves * 64) void readMfmaKernel(int iters, float* sink, Stamp* out) {
+    extern __shared__ __attribute__((aligned(1024))) char lds[];
+    _Float16* h = reinterpret_cast<_Float16*>(lds);
+    for (int i = threadIdx.x; i < 8192; i += blockDim.x) h[i] = (_Float16)(1.0f + 0.0001f * float(i & 63));
+    const int lane = threadIdx.x % 64;
+    int addr[Ilp];
+#pragma unroll
+    for (int j = 0; j < Ilp; ++j) {
+        const int row = (j % 4) * 32 + lane % 32;
+        addr[j] = ridge::swizzleA(row * 8 + 2 * (j / 4) + lane / 32) * 16;
+    }
+    half8_t b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = (_Float16)(1.0f - 0.001f * float((lane + i) & 7));
+    float16_t acc[Ilp];
+#pragma unroll
+    for (int j = 0; j < Ilp; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+    __syncthreads();
+    const uint64_t c0 = cycles();
+    const uint64_t r0 = realtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < Ilp; ++j) {
+            const half8_t a = *(const __attribute__((address_space(3))) half8_t*)(lds + addr[j]);
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+        }
+        asm volatile("" ::: "memory");
+    }
+    __syncthreads();
+    const uint64_t c1 = cycles();
+    const uint64_t r1 = realtime();
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < Ilp; ++j) s += acc[j][0] + acc[j][15];
+    if (s == 1.2345678e30f) sink[0] = s;
+    if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
+}
+
+template <int Waves, int Ilp>
+double mfmaPerCycle(int cus, float* dSink, Stamp* dStamps) {
+    auto k = readMfmaKernel<Waves, Ilp>;
+    CAL_HIP_CHECK(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kOneWorkgroupLds));
+    hipLaunchKernelGGL(k, dim3(cus), dim3(Waves * 64), kOneWorkgroupLds, nullptr, kIters, dSink, dStamps);
+    CAL_HIP_CHECK(hipGetLastError());
+    CAL_HIP_CHECK(hipDeviceSynchronize());
+    std::vector<Stamp> st(cus);
+    CAL_HIP_CHECK(hipMemcpy(st.data(), dStamps, cus * sizeof(Stamp), hipMemcpyDeviceToHost));
+    double cyc = 0.0, hz = 0.0;
+    medianStamps(st, cyc, hz);
+    return double(Waves) * kIters * Ilp / cyc;
+}
+
+}  // namespace
+
+int main() {
+    const hipDeviceProp_t prop = deviceBanner();
+    const int cus = prop.multiProcessorCount;
+    float* dSink = nullptr;
+    Stamp* dStamps = nullptr;
+    CAL_HIP_CHECK(hipMalloc(&dSink, sizeof(float)));
+    CAL_HIP_CHECK(hipMalloc(&dStamps, cus * sizeof(Stamp)));
+    warmUp();
+
+    constexpr int kWaves[] = {1, 2, 4, 8, 16};
+    constexpr int kIlps[] = {1, 2, 4, 8};
+    double surface[4][5] = {};
+    std::vector<double> reps[4][5];
+#define CAL_CELL(IC, WI, W, ILP)                                                         \
+    do {                                                                                 \
+        for (int r = 0; r < kRepeats; ++r) reps[IC][WI].push_back(mfmaPerCycle<W, ILP>(cus, dSink, dStamps)); \
+        surface[IC][WI] = median(reps[IC][WI]);                                          \
+    } while (0)
+#define CAL_COLUMN(IC, ILP) \
+    CAL_CELL(IC, 0, 1, ILP); CAL_CELL(IC, 1, 2, ILP); CAL_CELL(IC, 2, 4, ILP); CAL_CELL(IC, 3, 8, ILP)
+    CAL_COLUMN(0, 1);
+    CAL_CELL(0, 4, 16, 1);
+    CAL_COLUMN(1, 2);
+    CAL_CELL(1, 4, 16, 2);
+    CAL_COLUMN(2, 4);
+    CAL_CELL(2, 4, 16, 4);
+    CAL_COLUMN(3, 8);
+#undef CAL_COLUMN
+#undef CAL_CELL
+
+    double best[4] = {};
+    for (int c = 0; c < 4; ++c)
+        for (int w = 0; w < 5; ++w) best[c] = std::max(best[c], surface[c][w]);
+    std::printf("\nds_read_b128 -> v_mfma_f32_32x32x16_f16 chains: MFMA per cycle per CU (%% of column best)\n");
+    std::printf("  %5s %20s %20s %20s %20s\n", "waves", "ILP=1", "ILP=2", "ILP=4", "ILP=8");
+    for (int w = 0; w < 5; ++w) {
+        std::printf("  %5d", kWaves[w]);
+        for (int c = 0; c < 4; ++c) {
+            if (surface[c][w] > 0)
+                std::printf("   %9.4f (%5.1f%%)", surface[c][w], 100.0 * surface[c][w] / best[c]);
+            else
+                std::printf("   %18s", "-");
+        }
+        std::printf("\n");
+    }
+    for (int c = 0; c < 4; ++c)
+        for (int w = 0; w < 5; ++w)
+            if (surface[c][w] > 0)
+                std::printf("CAL_SURFACE ilp %d waves %d mfmaPerCycle %.6f\n", kIlps[c], kWaves[w], surface[c][w]);
+    int needed[4];
+    for (int c = 0; c < 4; ++c) {
+        needed[c] = kWaves[4];
+        for (int w = 0; w < 5; ++w)
+            if (surface[c][w] >= kSaturation * best[c]) {
+                needed[c] = kWaves[w];
+                break;
+            }
+        std::printf("  ILP=%d saturates at %2d waves/CU\n", kIlps[c], needed[c]);
+        std::printf("CAL_SATURATION ilp %d waves %d\n", kIlps[c], needed[c]);
+    }
+    int wBest = 0;
+    for (int w = 0; w < 5; ++w)
+        if (surface[1][w] == best[1]) wBest = w;
+    std::printf("\n");
+    reportConstant("warpsNeededToHide", double(needed[1]), "waves/CU", reps[1][wBest]);
+    std::printf("  the reported constant is the ILP=2 column, a threshold on a smooth curve\n");
+    std::printf("\nCAL_RESULT warpsNeededToHide %d\n", needed[1]);
+    CAL_HIP_CHECK(hipFree(dSink));
+    CAL_HIP_CHECK(hipFree(dStamps));
+    return 0;
+}

@@ -1,0 +1,94 @@
+"""Registered sweep shapes for the MI355X ground-truth measurement.
+
+    python -m ridge_amd.sweep [--seed S] [--out data/sweep/mi355x-registered.csv]
+
+The reference registers 14 hand-picked A100 shapes before measuring anything
+(data/sweep/phase4-registered.csv:1-52). Here the 14 shapes are drawn from a
+fixed seed: M and N from {1024, 2048, 4096, 8192, 16384}, K from
+{128, 1024, 4096, 8192}, element i of the draw being splitmix64(seed, i) modulo
+the set size (three draws per shape, duplicates redrawn). Every M and N is a
+multiple of 256 and every K of 64, so every registered variant divides every
+shape. The file is written once and committed before the first measurement;
+changing it afterwards is a visible, separate commit.
+"""
+
+import argparse
+import os
+
+MN_CHOICES = (1024, 2048, 4096, 8192, 16384)
+K_CHOICES = (128, 1024, 4096, 8192)
+DEFAULT_SEED = 0x5EED2026
+M64 = (1 << 64) - 1
+
+
+def splitmix64_at(seed, i):
+    z = (seed + (i + 1) * 0x9E3779B97F4A7C15) & M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+    return z ^ (z >> 31)
+
+
+def registered_shapes(seed=DEFAULT_SEED, count=14):
+    shapes, i = [], 0
+    while len(shapes) < count:
+        M = MN_CHOICES[splitmix64_at(seed, i) % len(MN_CHOICES)]
+        N = MN_CHOICES[splitmix64_at(seed, i + 1) % len(MN_CHOICES)]
+        K = K_CHOICES[splitmix64_at(seed, i + 2) % len(K_CHOICES)]
+        i += 3
+        if (M, N, K) not in shapes:
+            shapes.append((M, N, K))
+    return shapes
+
+
+def rationale(M, N, K):
+    tiles = (M // 256) * (N // 256)
+    return ("%d workgroups at 256x256 = %.2f waves over 256 CUs; %d K-tiles at BK=64; "
+            "%.1f FLOP/B compulsory" % (tiles, tiles / 256.0, K // 64,
+                                        2.0 * M * N * K / (2.0 * (M * K + K * N + M * N))))
+
+
+# The BASELINE.json configs measured beside the sweep (not part of the regret set).
+BASELINE_SHAPES = [
+    (1024, 1024, 1024, "baseline-1024cube"),
+    (4096, 4096, 4096, "baseline-4096cube-headline"),
+    (8192, 8192, 128, "baseline-small-k"),
+    (16384, 128, 8192, "baseline-tall-skinny"),
+]
+
+
+def write_registered(path, seed=DEFAULT_SEED):
+    lines = [
+        "# MI355X registered sweep: 14 shapes drawn by ridge_amd/sweep.py with seed 0x%X." % seed,
+        "# Registered before any measurement. The tile configs are the kernel table",
+        "# (ridge_amd/csrc/gemm_variants.def); the sweep is every shape x every variant.",
+        "# M,N,K,tag,rationale",
+    ]
+    for i, (M, N, K) in enumerate(registered_shapes(seed)):
+        lines.append("%d,%d,%d,s%02d-%dx%dx%d,%s" % (M, N, K, i, M, N, K, rationale(M, N, K)))
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def write_baseline(path):
+    lines = ["# BASELINE.json configs, measured over the variants that divide each.", "# M,N,K,tag,rationale"]
+    for M, N, K, tag in BASELINE_SHAPES:
+        lines.append("%d,%d,%d,%s,%s" % (M, N, K, tag, rationale(M, N, K) if N >= 256 else
+                                         "N=128: one column of 128-wide tiles, A streamed once"))
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--seed", type=lambda s: int(s, 0), default=DEFAULT_SEED)
+    ap.add_argument("--out", default="data/sweep/mi355x-registered.csv")
+    ap.add_argument("--baseline-out", default="data/sweep/mi355x-baseline-configs.csv")
+    args = ap.parse_args(argv)
+    os.makedirs(os.path.dirname(args.out) or ".", exist_ok=True)
+    write_registered(args.out, args.seed)
+    write_baseline(args.baseline_out)
+    print("wrote", args.out, "and", args.baseline_out)
+
+
+if __name__ == "__main__":
+    main()
