@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0
 DEFAULT_SHAPE = (4096, 4096, 4096)
 # The registered variant the sweep measured fastest at 4096^3.
 DEFAULT_VARIANT = (256, 256, 64, 128, 64, 2, 8)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_4096_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemmMfma_256x256x64w128x64s2g8_4096cube_traffic.json")
 
 
 def parse_ints(s, n):
@@ -85,6 +85,26 @@ def cpu_baseline(M, N, K, seconds=10.0):
     tflops = 2.0 * rows * N * K / dt / 1e12
     return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": "%d of %d output rows of %dx%dx%d (f64 accumulate, %.1f s)" % (rows, M, M, N, K, dt)}
+
+
+def cpu_baseline_naive_1core(n=1024, seconds=2.0):
+    """The reference's own CPU path, faithfully: the naive single-threaded i-j-k
+    f64 loop (check-gemm.cu:98-108) at 1024^3, where the reference uses it, on a
+    block of output rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    Ab = O.uniform_fill_f16(n * n, 1).reshape(n, n)
+    Bb = O.uniform_fill_f16(n * n, 2)
+    rows = 4
+    while True:
+        t0 = time.perf_counter()
+        O.gemm_f64(Ab[:rows].ravel(), Bb, rows, n, n, naive=True)
+        dt = time.perf_counter() - t0
+        if dt >= 0.5 * seconds or rows >= n:
+            break
+        rows = int(min(n, max(2 * rows, rows * seconds / max(dt, 1e-4))))
+    return {"value": round(2.0 * rows * n * n / dt / 1e12, 9), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": "%d of %d output rows of %d^3, naive i-j-k f64 loop (%.2f s)" % (rows, n, n, dt)}
 
 
 def run_copy_mode(steps):
@@ -220,6 +240,7 @@ def main():
                             "frac_of_hipblaslt": round(value / best, 4)}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)
+        out["cpu_baseline_naive_1core"] = cpu_baseline_naive_1core()
     print(json.dumps(out), flush=True)
 
 
