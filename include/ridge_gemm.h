@@ -50,6 +50,7 @@ typedef struct ridge_gemm_variant {
     int sgprs;           /* scalar registers per wave */
     int scratchBytes;    /* private segment bytes per lane (0 = no spills) */
     int occupancy;       /* waves per SIMD the compiler reports */
+    int pingPong;        /* 1: ping-pong schedule (8 wavefronts, >= 3 stages); 0: uniform */
 } ridge_gemm_variant_t;
 
 /* Number of rows in the table (the reference's numVariants(), gemm-mma.cu:121). */

@@ -18,14 +18,25 @@ namespace {
 
 typedef hipError_t (*LaunchFn)(const void*, const void*, void*, int, int, int, hipStream_t);
 
+// Schedule choice, a function of the tile config: eight wavefronts (two per
+// SIMD) with a ring of three or more stages run the ping-pong schedule, every
+// other variant the uniform one.
+constexpr bool usesPingPong(int waves, int stages) { return waves == 8 && stages >= 3; }
+
 template <int BM, int BN, int BK, int WM, int WN, int S, int G>
 hipError_t launchVariant(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t stream) {
     using T = ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>;
     const dim3 grid((unsigned)((M / BM) * (N / BN)));
     const dim3 block(T::kThreads);
-    hipLaunchKernelGGL((ridge::gemmMfmaKernel<BM, BN, BK, WM, WN, S, G>), grid, block, 0, stream,
-                       static_cast<const _Float16*>(A), static_cast<const _Float16*>(B),
-                       static_cast<_Float16*>(C), M, N, K);
+    if constexpr (usesPingPong(T::kWaves, S)) {
+        hipLaunchKernelGGL((ridge::gemmMfmaPingPongKernel<BM, BN, BK, WM, WN, S, G>), grid, block, 0, stream,
+                           static_cast<const _Float16*>(A), static_cast<const _Float16*>(B),
+                           static_cast<_Float16*>(C), M, N, K);
+    } else {
+        hipLaunchKernelGGL((ridge::gemmMfmaKernel<BM, BN, BK, WM, WN, S, G>), grid, block, 0, stream,
+                           static_cast<const _Float16*>(A), static_cast<const _Float16*>(B),
+                           static_cast<_Float16*>(C), M, N, K);
+    }
     return hipGetLastError();
 }
 
@@ -34,6 +45,7 @@ struct Entry {
     int ldsBytes;
     int threads;
     int waves;
+    int pingPong;
     LaunchFn launch;
 };
 
@@ -42,6 +54,7 @@ struct Entry {
           ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kLdsBytes,                            \
           ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kThreads,                             \
           ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kWaves,                               \
+          usesPingPong(ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kWaves, S) ? 1 : 0,       \
           &launchVariant<BM, BN, BK, WM, WN, S, G>},
 
 const Entry kTable[] = {
@@ -66,7 +79,7 @@ int ridge_gemm_get_variant(int i, ridge_gemm_variant_t* out) {
     std::memset(&v, 0, sizeof(v));
     v.BM = e.BM; v.BN = e.BN; v.BK = e.BK; v.WM = e.WM; v.WN = e.WN;
     v.stages = e.stages; v.groupM = e.groupM;
-    v.ldsBytes = e.ldsBytes; v.threads = e.threads; v.waves = e.waves;
+    v.ldsBytes = e.ldsBytes; v.threads = e.threads; v.waves = e.waves; v.pingPong = e.pingPong;
     if (i < ridge_gemm_resource_count) {
         const ridge_gemm_resources_t& r = ridge_gemm_resource_table[i];
         v.vgprs = r.vgprs; v.agprs = r.agprs; v.sgprs = r.sgprs;
@@ -110,14 +123,14 @@ int ridge_gemm_launch(int i, const void* A, const void* B, void* C, int M, int N
 
 size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {
     std::string s = "idx,BM,BN,BK,WM,WN,stages,groupM,ldsBytes,threads,regsPerThread,waves,vgprs,agprs,sgprs,"
-                    "scratchBytes,occupancy\n";
+                    "scratchBytes,occupancy,pingPong\n";
     char line[256];
     for (int i = 0; i < kNumVariants; ++i) {
         ridge_gemm_variant_t v;
         ridge_gemm_get_variant(i, &v);
-        std::snprintf(line, sizeof(line), "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d\n", i, v.BM, v.BN,
+        std::snprintf(line, sizeof(line), "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d\n", i, v.BM, v.BN,
                       v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes, v.threads, v.regsPerThread, v.waves,
-                      v.vgprs, v.agprs, v.sgprs, v.scratchBytes, v.occupancy);
+                      v.vgprs, v.agprs, v.sgprs, v.scratchBytes, v.occupancy, v.pingPong);
         s += line;
     }
     if (buf != nullptr && cap > 0) {
@@ -129,7 +142,8 @@ size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {
 }
 
 const char* ridge_gemm_build_info(void) {
-    return "ridge_gemm gfx950 mfma_f32_32x32x16_f16 direct-to-LDS ring, tr16 B reads, xcd+groupM order";
+    return "ridge_gemm gfx950 mfma_f32_32x32x16_f16, direct-to-LDS ring, tr16 B reads, xcd+groupM order, "
+           "ping-pong schedule for 8-wave rings of 3+ stages";
 }
 
 }  // extern "C"

@@ -40,6 +40,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace ridge {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -103,6 +106,29 @@ __device__ __forceinline__ int xcdRemap(int pid, int n) {
     return x * q + (x < r ? x : r) + pid / kXcds;
 }
 
+// Direct-to-LDS 16-byte load: lane t of the wave writes LDS bytes
+// [ldsAddr + 16 t, +16) with the 16 bytes at base + offset. base and ldsAddr are
+// wave-uniform (scalar registers; ldsAddr is carried in M0), offset is the lane's
+// 32-bit byte offset, so issuing a load costs no vector ALU instruction.
+//
+// Issued through inline asm on purpose. Seen as the builtin, the compiler's
+// wait-count pass treats the DMA as an LDS write that may alias later LDS reads
+// and puts an `s_waitcnt vmcnt(0)` in front of the transposing B reads, which
+// drains every prefetch in flight and serialises the ring. The kernels count
+// vmcnt themselves (waitVmcnt) and order LDS with barriers, so the compiler
+// needs no view of the DMA. The s_nop covers the M0-write -> LDS-DMA hazard the
+// compiler would otherwise insert.
+__device__ __forceinline__ void globalLoadLds16(const void* base, uint32_t offset, uint32_t ldsAddr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(offset), "s"(base), "{m0}"(ldsAddr)
+                 : "memory");
+}
+
+// LDS byte address of a __shared__ object, as a wave-uniform scalar.
+__device__ __forceinline__ uint32_t ldsAddress(const void* p) {
+    return __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const RIDGE_LDS_AS char*)(static_cast<const char*>(p)));
+}
+
 // s_waitcnt with only the vector-memory counter constrained. The memory clobber
 // keeps the compiler from moving LDS or global accesses across it.
 template <int N>
@@ -132,12 +158,19 @@ struct GemmTraits {
     static constexpr int kBytesB = BK * BN * 2;
     static constexpr int kStageBytes = kBytesA + kBytesB;
     static constexpr int kLdsBytes = STAGES * kStageBytes;
+    // LDS layout: the A tiles of all stages, then the B tiles of all stages, so a
+    // fragment read's stage offset is a small compile-time immediate.
+    static constexpr int kRegionA = STAGES * kBytesA;
     // 64-lane x 16-byte direct-to-LDS instructions per stage, and per wave.
     static constexpr int kInstA = kBytesA / 1024;
     static constexpr int kInstB = kBytesB / 1024;
     static constexpr int kPerWaveA = kInstA / kWaves;
     static constexpr int kPerWaveB = kInstB / kWaves;
     static constexpr int kLoadsPerTile = kPerWaveA + kPerWaveB;
+    // Byte distance between the k-steps of a B fragment and between its two
+    // 4-row halves.
+    static constexpr int kBStepBytes = kMfmaK * BN * 2;
+    static constexpr int kBHalfBytes = 4 * BN * 2;
 
     static_assert(STAGES >= 2, "the ring needs at least two LDS buffers");
     static_assert(BM % WM == 0 && BN % WN == 0, "workgroup tile must split into wave tiles");
@@ -152,163 +185,217 @@ struct GemmTraits {
     static_assert(kLdsBytes <= 163840, "LDS is 160 KiB per workgroup on gfx950");
 };
 
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1, so loop bodies see
+// their index as a compile-time constant.
+template <typename F, int... Is>
+__device__ __forceinline__ void staticForImpl(F& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void staticFor(F&& f) {
+    staticForImpl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Per-workgroup state and the operations both schedules are built from: the
+// output tile, the direct-to-LDS refill of a stage, the fragment reads of a
+// k-step, the MFMAs of a k-step and the epilogue.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUPM>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * kWaveSize)
-void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
-                    _Float16* __restrict__ C, int M, int N, int K) {
+struct GemmBlock {
     using T = GemmTraits<BM, BN, BK, WM, WN, STAGES, GROUPM>;
-    constexpr int TM = T::kTilesM;
-    constexpr int TN = T::kTilesN;
-    constexpr int CPR_A = T::kChunksPerRowA;
-    constexpr int CPR_B = T::kChunksPerRowB;
+    static constexpr int TM = T::kTilesM;
+    static constexpr int TN = T::kTilesN;
+    static constexpr int KS = T::kSteps;
+    static constexpr int CPR_A = T::kChunksPerRowA;
+    static constexpr int CPR_B = T::kChunksPerRowB;
 
-    __shared__ __attribute__((aligned(1024))) char lds[T::kLdsBytes];
+    const char* lds;      // the workgroup's LDS array (generic pointer to it)
+    uint32_t ldsBase;     // its LDS byte address (scalar)
+    int lane, wave, waveM, waveN;
+    int blockRow, blockCol;
+    const char* gA;       // A + blockRow * K (bytes), scalar
+    const char* gB;       // B + blockCol (bytes), scalar
+    size_t tileStrideB;   // bytes between K tiles of B: BK * N * 2
+    uint32_t offA[T::kPerWaveA];  // lane byte offsets of this wave's loads
+    uint32_t offB[T::kPerWaveB];
+    int rdA[TM][KS];      // A fragment byte offsets within an A tile
+    int rdB[TN];          // B fragment byte offsets within the B region
+    float16_t acc[TM][TN];
 
-    const int lane = threadIdx.x % kWaveSize;
-    // Wave index as a scalar: every lane of a wave agrees, and the LDS base of a
-    // direct-to-LDS load must be wave-uniform.
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-    const int waveM = wave / T::kWavesN;
-    const int waveN = wave % T::kWavesN;
+    __device__ __forceinline__ GemmBlock(const char* ldsArray, const _Float16* A, const _Float16* B, int M,
+                                         int N, int K) {
+        lds = ldsArray;
+        ldsBase = ldsAddress(ldsArray);
+        lane = threadIdx.x % kWaveSize;
+        // Wave index as a scalar: every lane agrees, and load bases must be uniform.
+        wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+        waveM = wave / T::kWavesN;
+        waveN = wave % T::kWavesN;
 
-    // Output tile for this workgroup.
-    const int numPidM = M / BM;
-    const int numPidN = N / BN;
-    const int pid = xcdRemap(blockIdx.x, gridDim.x);
-    const int pidInGroup = pid % (GROUPM * numPidN);
-    const int firstPidM = (pid / (GROUPM * numPidN)) * GROUPM;
-    const int groupRows = min(numPidM - firstPidM, GROUPM);
-    const int pidM = firstPidM + pidInGroup % groupRows;
-    const int pidN = pidInGroup / groupRows;
-    const int blockRow = pidM * BM;
-    const int blockCol = pidN * BN;
+        // XCD remap, then the GroupM launch order (reference gemm-mma.cuh:158-178).
+        const int numPidM = M / BM;
+        const int numPidN = N / BN;
+        const int pid = xcdRemap(blockIdx.x, gridDim.x);
+        const int pidInGroup = pid % (GROUPM * numPidN);
+        const int firstPidM = (pid / (GROUPM * numPidN)) * GROUPM;
+        const int groupRows = min(numPidM - firstPidM, GROUPM);
+        blockRow = (firstPidM + pidInGroup % groupRows) * BM;
+        blockCol = (pidInGroup / groupRows) * BN;
 
-    // Per-lane global element offsets of this wave's direct-to-LDS loads,
-    // relative to the tile origin. Wave instruction j fills physical chunks
-    // [64 j, 64 j + 64) of a stage; lane t's chunk holds logical chunk
-    // swizzle(64 j + t).
-    int offA[T::kPerWaveA];
-    int offB[T::kPerWaveB];
-#pragma unroll
-    for (int i = 0; i < T::kPerWaveA; ++i) {
-        const int j = i * T::kWaves + wave;
-        const int q = swizzleA(j * 64 + lane);
-        offA[i] = (q / CPR_A) * K + (q % CPR_A) * 8;
-    }
-#pragma unroll
-    for (int i = 0; i < T::kPerWaveB; ++i) {
-        const int j = i * T::kWaves + wave;
-        const int q = swizzleB<CPR_B>(j * 64 + lane);
-        offB[i] = (q / CPR_B) * N + (q % CPR_B) * 8;
-    }
-    const _Float16* gA = A + (size_t)blockRow * K;
-    const _Float16* gB = B + blockCol;
-
-    auto issueTile = [&](int kTile, int stage) {
-        const _Float16* srcA = gA + kTile * BK;
-        const _Float16* srcB = gB + (size_t)kTile * BK * N;
-        char* dst = lds + stage * T::kStageBytes;
+        gA = reinterpret_cast<const char*>(A + (size_t)blockRow * K);
+        gB = reinterpret_cast<const char*>(B + blockCol);
+        tileStrideB = (size_t)BK * N * 2;
+        // Wave instruction j fills physical chunks [64 j, 64 j + 64) of a tile;
+        // lane t's chunk holds logical chunk swizzle(64 j + t).
 #pragma unroll
         for (int i = 0; i < T::kPerWaveA; ++i) {
-            const int j = i * T::kWaves + wave;
-            __builtin_amdgcn_global_load_lds((const void*)(srcA + offA[i]),
-                                             (RIDGE_LDS_AS void*)(dst + j * 1024), 16, 0, 0);
+            const int q = swizzleA((i * T::kWaves + wave) * 64 + lane);
+            offA[i] = (uint32_t)(((q / CPR_A) * K + (q % CPR_A) * 8) * 2);
         }
 #pragma unroll
         for (int i = 0; i < T::kPerWaveB; ++i) {
-            const int j = i * T::kWaves + wave;
-            __builtin_amdgcn_global_load_lds((const void*)(srcB + offB[i]),
-                                             (RIDGE_LDS_AS void*)(dst + T::kBytesA + j * 1024), 16, 0, 0);
+            const int q = swizzleB<CPR_B>((i * T::kWaves + wave) * 64 + lane);
+            offB[i] = (uint32_t)(((q / CPR_B) * N + (q % CPR_B) * 8) * 2);
         }
-    };
-
-    // Fragment read offsets (bytes, within a stage).
-    // A: tile tm, k-step ks: row = waveM*WM + tm*32 + lane%32, chunk = 2 ks + lane/32.
-    int rdA[TM][T::kSteps];
+        // A fragment of tile tm, k-step ks: row waveM*WM + 32 tm + lane%32,
+        // logical chunk 2 ks + lane/32.
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
+        for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int ks = 0; ks < T::kSteps; ++ks) {
-            const int row = waveM * WM + tm * kMfmaM + lane % 32;
-            rdA[tm][ks] = swizzleA(row * CPR_A + 2 * ks + lane / 32) * 16;
+            for (int ks = 0; ks < KS; ++ks)
+                rdA[tm][ks] = swizzleA((waveM * WM + tm * kMfmaM + lane % 32) * CPR_A + 2 * ks + lane / 32) * 16;
+        // B fragment of tile tn: 16-lane group g = lane/16, s = lane%16 reads row
+        // 8 (g/2) + s/4 (+16 ks + 4 h), columns waveN*WN + 32 tn + 16 (g%2) + 4 (s%4).
+        // Rows enter the swizzle only through row % 4 = s/4, so k-step and half
+        // offsets stay outside the XOR as compile-time immediates.
+        {
+            const int g = lane / 16;
+            const int s = lane % 16;
+            const int rowLane = 8 * (g / 2) + s / 4;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int col = waveN * WN + tn * kMfmaN + 16 * (g % 2) + 4 * (s % 4);
+                rdB[tn] = T::kRegionA + swizzleB<CPR_B>(rowLane * CPR_B + col / 8) * 16 + (col % 8) * 2;
+            }
         }
-    }
-    // B: tile tn, k-step ks, half h: 16-lane group g = lane/16, s = lane%16 reads
-    // row 16 ks + 8 (g/2) + 4 h + s/4, columns waveN*WN + 32 tn + 16 (g%2) + 4 (s%4).
-    // Rows enter the swizzle only through row % 4 = s/4, so the row term adds
-    // outside the XOR as a compile-time offset.
-    int rdB[TN];
-    {
-        const int g = lane / 16;
-        const int s = lane % 16;
-        const int rowLane = 8 * (g / 2) + s / 4;
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-            const int col = waveN * WN + tn * kMfmaN + 16 * (g % 2) + 4 * (s % 4);
-            const int q = swizzleB<CPR_B>(rowLane * CPR_B + col / 8);
-            rdB[tn] = T::kBytesA + q * 16 + (col % 8) * 2;
-        }
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[tm][tn][e] = 0.0f;
     }
 
-    float16_t acc[TM][TN];
+    // Refills LDS stage `stage` with K tile kTile (this wave's share). No vector
+    // ALU work: scalar tile bases, constant lane offsets, M0 from scalars.
+    __device__ __forceinline__ void issueTile(int kTile, int stage) const {
+        const char* srcA = gA + (size_t)kTile * BK * 2;
+        const char* srcB = gB + (size_t)kTile * tileStrideB;
+        const uint32_t dstA = ldsBase + stage * T::kBytesA;
+        const uint32_t dstB = ldsBase + T::kRegionA + stage * T::kBytesB;
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+        for (int i = 0; i < T::kPerWaveA; ++i) globalLoadLds16(srcA, offA[i], dstA + (i * T::kWaves + wave) * 1024);
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[tm][tn][e] = 0.0f;
+        for (int i = 0; i < T::kPerWaveB; ++i) globalLoadLds16(srcB, offB[i], dstB + (i * T::kWaves + wave) * 1024);
+    }
 
-    const int numK = K / BK;
-
-    // Operand fragments of one k-step: TM A reads (ds_read_b128) and 2 TN
-    // transposing B reads.
-    auto readFrags = [&](const char* base, int ks, half8_t (&a)[TM], half8_t (&b)[TN]) {
+    // Fragments of k-step ks of the tile in LDS stage STAGE (compile-time, so the
+    // stage offset folds into the DS instruction's immediate).
+    template <int STAGE>
+    __device__ __forceinline__ void readFrags(int ks, half8_t (&a)[TM], half8_t (&b)[TN]) const {
+        const RIDGE_LDS_AS char* l = (const RIDGE_LDS_AS char*)(lds);
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm) {
-            a[tm] = *(const RIDGE_LDS_AS half8_t*)(base + rdA[tm][ks]);
-        }
+        for (int tm = 0; tm < TM; ++tm)
+            a[tm] = *(const RIDGE_LDS_AS half8_t*)(l + rdA[tm][ks] + STAGE * T::kBytesA);
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-            const char* p = base + rdB[tn] + ks * 16 * CPR_B * 16;
-            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RIDGE_LDS_AS short4_t*)(p));
-            const short4_t hi =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((RIDGE_LDS_AS short4_t*)(p + 4 * CPR_B * 16));
-            const half4_t l4 = __builtin_bit_cast(half4_t, lo);
-            const half4_t h4 = __builtin_bit_cast(half4_t, hi);
+            const RIDGE_LDS_AS char* p = l + rdB[tn] + STAGE * T::kBytesB + ks * T::kBStepBytes;
+            const half4_t l4 = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                               (RIDGE_LDS_AS short4_t*)(p)));
+            const half4_t h4 = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                               (RIDGE_LDS_AS short4_t*)(p + T::kBHalfBytes)));
             b[tn] = half8_t{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
         }
-    };
-    auto mfmaStep = [&](const half8_t (&a)[TM], const half8_t (&b)[TN]) {
+    }
+
+    // One k-step of MFMAs, B fragment in the first operand (transposed C tile).
+    __device__ __forceinline__ void mfmaStep(const half8_t (&a)[TM], const half8_t (&b)[TN]) {
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
                 acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
-    };
-    // Scheduling hint for one k-step: alternate one MFMA with one LDS read so
-    // the reads of the next k-step hide under this step's matrix work.
-    auto interleave = [&]() {
-#if RIDGE_GEMM_SCHED
-        constexpr int kMfmas = TM * TN;
-        constexpr int kReads = TM + 2 * TN;
-#pragma unroll
-        for (int i = 0; i < kMfmas; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        if (kReads > kMfmas) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kMfmas, 0);
-#endif
-    };
-
-    // Prologue: every stage filled (tiles 0 .. STAGES-1). A tile that does not
-    // exist is not issued; the waits count only issued loads, and near the end of
-    // K fewer were issued, so those waits drain fully.
-#pragma unroll
-    for (int s = 0; s < STAGES; ++s) {
-        if (s < numK) issueTile(s, s);
     }
+
+    // FP32 -> FP16 (nearest even), 8-byte stores of four consecutive columns,
+    // one MFMA tile at a time.
+    __device__ __forceinline__ void store(_Float16* C, int N) const {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            const int m = blockRow + waveM * WM + tm * kMfmaM + lane % 32;
+            _Float16* crow = C + (size_t)m * N;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int n0 = blockCol + waveN * WN + tn * kMfmaN + 4 * (lane / 32);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    half4_t v;
+                    v[0] = (_Float16)acc[tm][tn][4 * i + 0];
+                    v[1] = (_Float16)acc[tm][tn][4 * i + 1];
+                    v[2] = (_Float16)acc[tm][tn][4 * i + 2];
+                    v[3] = (_Float16)acc[tm][tn][4 * i + 3];
+                    *(half4_t*)(crow + n0 + 8 * i) = v;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+// Scheduling hint for one k-step of the uniform schedule: alternate one MFMA
+// with one LDS read so the reads of the next k-step hide under this step.
+template <int TM, int TN>
+__device__ __forceinline__ void interleaveHint() {
+#if RIDGE_GEMM_SCHED
+    constexpr int kMfmas = TM * TN;
+    constexpr int kReads = TM + 2 * TN;
+#pragma unroll
+    for (int i = 0; i < kMfmas; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if (kReads > kMfmas) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kMfmas, 0);
+#endif
+}
+
+// ---------------------------------------------------------------------------
+// Uniform schedule: every wavefront runs the same phase at the same time.
+// Fragments are double-buffered across k-steps; the tile boundary sits inside
+// the last k-step of a tile: once tile kt+1 has landed and every wave is past
+// its reads of tile kt, the freed stage is refilled with tile kt+STAGES and
+// tile kt+1's first fragments are read while tile kt's last MFMAs run.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUPM>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * kWaveSize)
+void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                    _Float16* __restrict__ C, int M, int N, int K) {
+    using T = GemmTraits<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    using Blk = GemmBlock<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    constexpr int TM = T::kTilesM;
+    constexpr int TN = T::kTilesN;
+    constexpr int KS = T::kSteps;
+    constexpr int L = T::kLoadsPerTile;
+
+    __shared__ __attribute__((aligned(1024))) char lds[T::kLdsBytes];
+    Blk blk(lds, A, B, M, N, K);
+    const int numK = K / BK;
+
+    // Prologue: every stage filled; a tile that does not exist is not issued,
+    // and the waits count only issued loads (near the end of K they drain fully).
+    staticFor<STAGES>([&](auto sC) {
+        if (sC.value < numK) blk.issueTile(sC.value, sC.value);
+    });
     if (numK >= STAGES) {
-        waitVmcnt<(STAGES - 1) * T::kLoadsPerTile>();
+        waitVmcnt<(STAGES - 1) * L>();
     } else {
         waitVmcnt<0>();
     }
@@ -316,66 +403,128 @@ void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__
 
     half8_t fa[2][TM];
     half8_t fb[2][TN];
-    readFrags(lds, 0, fa[0], fb[0]);
+    blk.template readFrags<0>(0, fa[0], fb[0]);
 
-    // Fragments are double-buffered across k-steps (kSteps is even, so the
-    // buffer parity is the same in every K tile). The tile boundary sits inside
-    // the last k-step: once tile kt+1 has landed and every wave is past its reads
-    // of tile kt, the freed stage is refilled with tile kt+STAGES and the first
-    // fragments of tile kt+1 are read while the last MFMAs of tile kt run.
-    int stage = 0;
-    for (int kt = 0; kt < numK; ++kt) {
-        const char* base = lds + stage * T::kStageBytes;
-        const int nextStage = (stage + 1 == STAGES) ? 0 : stage + 1;
+    for (int kt0 = 0; kt0 < numK; kt0 += STAGES) {
+        staticFor<STAGES>([&](auto sC) {
+            constexpr int s = sC.value;
+            constexpr int sNext = (s + 1) % STAGES;
+            const int kt = kt0 + s;
+            if (kt < numK) {
 #pragma unroll
-        for (int ks = 0; ks < T::kSteps; ++ks) {
-            const int cur = ks & 1;
-            if (ks + 1 < T::kSteps) {
-                readFrags(base, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
-            } else if (kt + 1 < numK) {
-                // Tile kt+1 has landed once at most tiles kt+2 .. kt+STAGES-1 are
-                // outstanding.
-                if (kt + STAGES - 1 < numK) {
-                    waitVmcnt<(STAGES - 2) * T::kLoadsPerTile>();
-                } else {
-                    waitVmcnt<0>();
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int cur = ks & 1;
+                    if (ks + 1 < KS) {
+                        blk.template readFrags<s>(ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                    } else if (kt + 1 < numK) {
+                        // Tile kt+1 has landed once at most tiles kt+2 .. kt+STAGES-1
+                        // are outstanding.
+                        if (kt + STAGES - 1 < numK) {
+                            waitVmcnt<(STAGES - 2) * L>();
+                        } else {
+                            waitVmcnt<0>();
+                        }
+                        // This wave's reads of tile kt are complete (lgkmcnt(0)) and
+                        // every wave arrived: stage s is free and tile kt+1 visible.
+                        barrierLds();
+                        if (kt + STAGES < numK) blk.issueTile(kt + STAGES, s);
+                        blk.template readFrags<sNext>(0, fa[cur ^ 1], fb[cur ^ 1]);
+                    }
+                    blk.mfmaStep(fa[cur], fb[cur]);
+                    interleaveHint<TM, TN>();
                 }
-                // This wave's reads of tile kt completed (lgkmcnt(0)) and every
-                // wave arrived, so stage `stage` is free and tile kt+1 is visible.
-                barrierLds();
-                if (kt + STAGES < numK) issueTile(kt + STAGES, stage);
-                readFrags(lds + nextStage * T::kStageBytes, 0, fa[cur ^ 1], fb[cur ^ 1]);
             }
-            mfmaStep(fa[cur], fb[cur]);
-            interleave();
-        }
-        stage = nextStage;
+        });
     }
+    blk.store(C, N);
+}
 
-    // Epilogue: FP32 -> FP16 (round to nearest even) and 8-byte stores of four
-    // consecutive columns. No LDS is touched, so no drain of the ring is needed
-    // beyond the final wait inside the loop.
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-        const int m = blockRow + waveM * WM + tm * kMfmaM + lane % 32;
-        _Float16* crow = C + (size_t)m * N;
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-            const int n0 = blockCol + waveN * WN + tn * kMfmaN + 4 * (lane / 32);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                half4_t v;
-                v[0] = (_Float16)acc[tm][tn][4 * i + 0];
-                v[1] = (_Float16)acc[tm][tn][4 * i + 1];
-                v[2] = (_Float16)acc[tm][tn][4 * i + 2];
-                v[3] = (_Float16)acc[tm][tn][4 * i + 3];
-                *(half4_t*)(crow + n0 + 8 * i) = v;
-            }
-            // One tile at a time: without this fence the scheduler hoists every
-            // accumulator read to the top of the epilogue and runs out of VGPRs.
-            __builtin_amdgcn_sched_barrier(0);
-        }
+// ---------------------------------------------------------------------------
+// Ping-pong schedule for 8-wavefront workgroups (two wavefronts per SIMD).
+//
+// Waves 0-3 (group 0) and 4-7 (group 1) land one per SIMD each (wave w and
+// w + 4 share a SIMD, probed with HW_ID). Both run the same body per K tile
+//     M-phase: refill this wave's share of the stage freed by tile kt-1 with
+//              tile kt+STAGES-1; read all of tile kt's fragments into VGPRs
+//     barrier
+//     C-phase: all MFMAs of tile kt (s_setprio 1)
+//     barrier
+// with group 1 one barrier behind, so on every SIMD one wave is in its matrix
+// phase while the other is in its memory phase. Every barrier is executed by all
+// eight waves (group 0 adds one at the end to match group 1's extra one at the
+// start).
+//
+// Hazards, with phases p = 0, 1, ...: group 0 reads tile t at p = 2t, group 1 at
+// p = 2t+1.
+//  * WAR: tile t+STAGES-1 overwrites the stage of tile t-1 and is issued at
+//    p = 2t (group 0) or 2t+1 (group 1), after both groups read tile t-1.
+//  * RAW: tile t+1 must be in LDS before barrier (2t+1 | 2t+2). Group 0 reaches
+//    it at the end of its C-phase and group 1 at the end of its M-phase; each
+//    waits there until at most tiles t+2 .. t+STAGES-1 of its own loads are
+//    outstanding.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUPM>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * kWaveSize)
+void gemmMfmaPingPongKernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                            _Float16* __restrict__ C, int M, int N, int K) {
+    using T = GemmTraits<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    using Blk = GemmBlock<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    static_assert(T::kWaves == 8, "ping-pong pairs two groups of four wavefronts");
+    static_assert(STAGES >= 3, "ping-pong refills one tile ahead of two in flight");
+    constexpr int TM = T::kTilesM;
+    constexpr int TN = T::kTilesN;
+    constexpr int KS = T::kSteps;
+    constexpr int L = T::kLoadsPerTile;
+
+    __shared__ __attribute__((aligned(1024))) char lds[T::kLdsBytes];
+    Blk blk(lds, A, B, M, N, K);
+    const int group = blk.wave / 4;
+    const int numK = K / BK;
+
+    staticFor<STAGES - 1>([&](auto sC) {
+        if (sC.value < numK) blk.issueTile(sC.value, sC.value);
+    });
+    if (numK >= STAGES - 1) {
+        waitVmcnt<(STAGES - 2) * L>();
+    } else {
+        waitVmcnt<0>();
     }
+    barrierLds();
+    if (group == 1) barrierLds();
+
+    for (int kt0 = 0; kt0 < numK; kt0 += STAGES) {
+        staticFor<STAGES>([&](auto sC) {
+            constexpr int s = sC.value;
+            constexpr int sRefill = (s + STAGES - 1) % STAGES;
+            const int kt = kt0 + s;
+            if (kt < numK) {
+                const bool steady = kt + STAGES - 1 < numK;
+                // M-phase.
+                if (steady) blk.issueTile(kt + STAGES - 1, sRefill);
+                half8_t fa[KS][TM];
+                half8_t fb[KS][TN];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) blk.template readFrags<s>(ks, fa[ks], fb[ks]);
+                if (group == 1) {
+                    if (steady) waitVmcnt<(STAGES - 2) * L>();
+                    else waitVmcnt<0>();
+                }
+                barrierLds();
+                // C-phase.
+                __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) blk.mfmaStep(fa[ks], fb[ks]);
+                __builtin_amdgcn_s_setprio(0);
+                if (group == 0) {
+                    if (steady) waitVmcnt<(STAGES - 2) * L>();
+                    else waitVmcnt<0>();
+                }
+                barrierLds();
+            }
+        });
+    }
+    if (group == 0) barrierLds();
+    blk.store(C, N);
 }
 
 }  // namespace ridge

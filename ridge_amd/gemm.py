@@ -37,7 +37,7 @@ class RidgeGemmError(RuntimeError):
 class _VariantStruct(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "BM", "BN", "BK", "WM", "WN", "stages", "groupM", "ldsBytes", "threads", "regsPerThread",
-        "waves", "vgprs", "agprs", "sgprs", "scratchBytes", "occupancy")]
+        "waves", "vgprs", "agprs", "sgprs", "scratchBytes", "occupancy", "pingPong")]
 
 
 @dataclass(frozen=True)
@@ -59,6 +59,7 @@ class Variant:
     sgprs: int
     scratchBytes: int
     occupancy: int
+    pingPong: int
 
     @property
     def smemBytes(self):
