@@ -35,8 +35,8 @@ PEAK_FP16_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0
 DEFAULT_SHAPE = (4096, 4096, 4096)
 # The registered variant the sweep measured fastest at 4096^3.
-DEFAULT_VARIANT = (256, 256, 64, 128, 64, 2, 8)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemmMfma_256x256x64w128x64s2g8_4096cube_traffic.json")
+DEFAULT_VARIANT = (256, 256, 32, 128, 64, 4, 4)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemmMfmaPingPong_256x256x32w128x64s4g4_4096cube_traffic.json")
 
 
 def parse_ints(s, n):

@@ -42,7 +42,7 @@ def test_table_has_24_registered_rows_with_consistent_fields():
     assert len(set(keys)) == 24
     for v in vs:
         assert v.BM in (64, 128, 256) and v.BN in (64, 128, 256) and v.BK in (32, 64)
-        assert 2 <= v.stages <= 4
+        assert 2 <= v.stages <= 5
         assert v.waves == (v.BM // v.WM) * (v.BN // v.WN)
         assert v.threads == 64 * v.waves
         assert v.ldsBytes == v.stages * (v.BM * v.BK + v.BK * v.BN) * 2
@@ -59,16 +59,16 @@ def test_no_variant_spills():
 
 
 def test_divisibility_and_bad_launches_are_rejected_before_any_gpu_call():
-    i = G.find_variant(256, 256, 64, 128, 64, 2, 8)
+    i = G.find_variant(256, 256, 32, 128, 64, 4, 4)
     v = G.variant(i)
     assert v.divides(4096, 4096, 4096)
-    assert not v.divides(4096, 4096, 4000)
+    assert not v.divides(4096, 4096, 4016)
     assert not v.divides(128, 4096, 4096)
     assert not v.divides(0, 256, 64)
     L = G.lib()
     # Non-dividing shape, null pointers, misaligned pointers and a bad index all
     # return hipErrorInvalidValue without touching a device.
-    assert L.ridge_gemm_launch(i, 4096, 4096, 4096, 4096, 4096, 4000, None) == G.HIP_ERROR_INVALID_VALUE
+    assert L.ridge_gemm_launch(i, 4096, 4096, 4096, 4096, 4096, 4016, None) == G.HIP_ERROR_INVALID_VALUE
     assert L.ridge_gemm_launch(i, None, 4096, 4096, 256, 256, 64, None) == G.HIP_ERROR_INVALID_VALUE
     assert L.ridge_gemm_launch(i, 4098, 4096, 4096, 256, 256, 64, None) == G.HIP_ERROR_INVALID_VALUE
     assert L.ridge_gemm_launch(999, 4096, 4096, 4096, 256, 256, 64, None) == G.HIP_ERROR_INVALID_VALUE

@@ -109,7 +109,7 @@ def test_small_integer_inputs_bit_exact_every_variant(M, N, K):
 
 def test_headline_4096_exact_integers_and_identity():
     M = N = K = 4096
-    best = G.find_variant(256, 256, 64, 128, 64, 2, 8)
+    best = G.find_variant(256, 256, 32, 128, 64, 4, 4)
     Ab, Bb, want = _exact_case(M, N, K, -2, 2, 4096)
     A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
     got = _bits(_run(best, A, B, M, N, K))
