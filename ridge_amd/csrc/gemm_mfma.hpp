@@ -18,15 +18,21 @@
 //    a ring; tile kt+STAGES-1 is in flight while tile kt is consumed, and the
 //    hand-counted `s_waitcnt vmcnt(n)` + `s_barrier` replaces __syncthreads(),
 //    whose fence would drain every outstanding prefetch.
-//  * LDS -> VGPR: A fragments are one `ds_read_b128` per lane (8 consecutive k of
-//    one row). B is stored as it sits in memory (n contiguous); its fragments are
-//    read with two `ds_read_b64_tr_b16` per 32x32 tile, the gfx950 transposing
-//    LDS read. Within a 16-lane group, lane s = 4j + r points at
-//    B[k0 + j][n0 + 4r .. n0 + 4r + 3] and lane i receives B[k0 .. k0 + 3][n0 + i].
-//  * MFMA: v_mfma_f32_32x32x16_f16 with the operands swapped (B fragment in the
-//    "A" slot), which yields the transposed accumulator: lane l holds
-//    C[m0 + l%32][n0 + 8i + 4(l/32) + j] in acc[4i + j]. Four consecutive columns
-//    per lane let the epilogue write 8-byte FP16 stores with no LDS round trip.
+//  * MFMA: v_mfma_f32_16x16x32_f16. At equal cycles per FLOP it draws less power
+//    than the 32x32x16 form; under a full-chip load with random operands the
+//    loaded clock measured 1.89 GHz against 1.65 GHz, and the whole-chip GEMM is
+//    power-limited, so the smaller instruction is the faster one.
+//  * LDS -> VGPR: an MFMA operand is 8 consecutive k of one row (A) or one column
+//    (B) per lane, lane group g = lane/16 holding k = 8g .. 8g+7 and lane%16 the
+//    row or column. A fragments are one `ds_read_b128` per lane. B is stored as
+//    it sits in memory (n contiguous); its fragments are read with two
+//    `ds_read_b64_tr_b16` per 16x32 tile, the gfx950 transposing LDS read: within
+//    a 16-lane group, lane s = 4j + r points at B[k0 + j][n0 + 4r .. n0 + 4r + 3]
+//    and lane i receives B[k0 .. k0 + 3][n0 + i].
+//  * The operands are swapped (B fragment in the instruction's A slot), which
+//    yields the transposed accumulator: lane l holds C[m0 + l%16][n0 + 4(l/16) + r]
+//    in acc[r]. Four consecutive columns per lane let the epilogue write 8-byte
+//    FP16 stores with no LDS round trip.
 //  * Workgroup order: the hardware deals workgroups round-robin over the 8 XCDs,
 //    each with its own L2. xcdRemap makes the workgroups of one XCD a contiguous
 //    range of the logical order, and the GroupM mapping of that logical order
@@ -48,7 +54,7 @@ namespace ridge {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
 #define RIDGE_LDS_AS __attribute__((address_space(3)))
 
@@ -59,10 +65,10 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kWaveSize = 64;
 constexpr int kXcds = 8;
-// MFMA instruction shape (v_mfma_f32_32x32x16_f16): 32768 FLOP per instruction.
-constexpr int kMfmaM = 32;
-constexpr int kMfmaN = 32;
-constexpr int kMfmaK = 16;
+// MFMA instruction shape (v_mfma_f32_16x16x32_f16): 16384 FLOP per instruction.
+constexpr int kMfmaM = 16;
+constexpr int kMfmaN = 16;
+constexpr int kMfmaK = 32;
 
 // ---------------------------------------------------------------------------
 // LDS swizzles. Both map a logical 16-byte chunk index to a physical one and are
@@ -80,20 +86,24 @@ __device__ __forceinline__ int swizzleA(int q) {
     return q ^ ((line ^ (line >> 3)) & 7);
 }
 
-// B tile, [BK][BN] halves, n contiguous, chunk q = k * (BN/8) + c. A transposing
-// read has 16 lanes cover 4 consecutive k rows x 2 chunks (and two groups cover
-// 4 rows x 4 chunks). The mask depends on k % 4: {0, 10, 4, 14} makes the 8
-// chunks of one group distinct modulo 8 and the 16 chunks of a group pair
-// distinct modulo 16; with only 8 chunks per row (BN = 64) it falls back to
-// {0, 2, 4, 6}, which must stay below the row length.
+// B tile, [BK][BN] halves, n contiguous, chunk q = k * (BN/8) + c. One
+// transposing read has each 16-lane group cover 4 consecutive k rows x 2 chunks,
+// the four groups at rows 8g + {0..3} (+ 4 for the second half of a fragment).
+// LDS serves these 8-byte reads 32 lanes (256 bytes) at a time, so the 16 chunks
+// of a group pair -- rows {r..r+3} and {r+8..r+11}, two chunks each -- must land
+// in 16 distinct 16-byte bank slots. The mask 2 * (k%4 + 4 * ((k/8)%2)) gives the
+// eight rows eight distinct even offsets, and the chunk pair fills the odd one.
+// With only 8 chunks per row (BN = 64) the row's own parity supplies bit 3 of the
+// slot, and the mask 2 * ((k/2)%2 + 2 * ((k/8)%2)) separates the rest; it stays
+// below the row length. The mask uses k bits 0, 1 and 3 only, so row offsets of
+// 4 (fragment half) and 32 (k-step) leave it unchanged.
 template <int CPR_B>
 __device__ __forceinline__ int swizzleB(int q) {
-    const int k4 = (q / CPR_B) & 3;
+    const int k = q / CPR_B;
     if constexpr (CPR_B >= 16) {
-        const int m = (k4 == 0) ? 0 : (k4 == 1) ? 10 : (k4 == 2) ? 4 : 14;
-        return q ^ m;
+        return q ^ (2 * ((k & 3) + 4 * ((k >> 3) & 1)));
     } else {
-        return q ^ (2 * k4);
+        return q ^ (2 * (((k >> 1) & 1) + 2 * ((k >> 3) & 1)));
     }
 }
 
@@ -149,9 +159,9 @@ struct GemmTraits {
     static constexpr int kWavesN = BN / WN;
     static constexpr int kWaves = kWavesM * kWavesN;
     static constexpr int kThreads = kWaves * kWaveSize;
-    static constexpr int kTilesM = WM / kMfmaM;   // MFMA tiles per wave along M
+    static constexpr int kTilesM = WM / kMfmaM;   // 16x16 MFMA tiles per wave along M
     static constexpr int kTilesN = WN / kMfmaN;   // ... along N
-    static constexpr int kSteps = BK / kMfmaK;    // MFMA k-steps per K tile
+    static constexpr int kSteps = BK / kMfmaK;    // 32-deep MFMA k-steps per K tile
     static constexpr int kChunksPerRowA = BK / 8;
     static constexpr int kChunksPerRowB = BN / 8;
     static constexpr int kBytesA = BM * BK * 2;
@@ -168,15 +178,14 @@ struct GemmTraits {
     static constexpr int kPerWaveB = kInstB / kWaves;
     static constexpr int kLoadsPerTile = kPerWaveA + kPerWaveB;
     // Byte distance between the k-steps of a B fragment and between its two
-    // 4-row halves.
+    // 4-row halves (k 8g..8g+3 and 8g+4..8g+7).
     static constexpr int kBStepBytes = kMfmaK * BN * 2;
     static constexpr int kBHalfBytes = 4 * BN * 2;
 
     static_assert(STAGES >= 2, "the ring needs at least two LDS buffers");
     static_assert(BM % WM == 0 && BN % WN == 0, "workgroup tile must split into wave tiles");
-    static_assert(WM % kMfmaM == 0 && WN % kMfmaN == 0, "wave tile must split into 32x32 MFMA tiles");
+    static_assert(WM % kMfmaM == 0 && WN % kMfmaN == 0, "wave tile must split into 16x16 MFMA tiles");
     static_assert(BK % kMfmaK == 0, "BK must be a whole number of MFMA k-steps");
-    static_assert(kSteps % 2 == 0, "fragment double-buffering assumes an even number of k-steps");
     static_assert(BK == 32 || BK == 64, "the A swizzle is derived for BK of 32 or 64");
     static_assert(BN == 64 || BN == 128 || BN == 256, "the B swizzle is derived for BN of 64, 128 or 256");
     static_assert(kBytesA % 1024 == 0 && kBytesB % 1024 == 0, "tiles must be whole 1 KiB wave loads");
@@ -219,7 +228,7 @@ struct GemmBlock {
     uint32_t offB[T::kPerWaveB];
     int rdA[TM][KS];      // A fragment byte offsets within an A tile
     int rdB[TN];          // B fragment byte offsets within the B region
-    float16_t acc[TM][TN];
+    float4_t acc[TM][TN];
 
     __device__ __forceinline__ GemmBlock(const char* ldsArray, const _Float16* A, const _Float16* B, int M,
                                          int N, int K) {
@@ -256,24 +265,25 @@ struct GemmBlock {
             const int q = swizzleB<CPR_B>((i * T::kWaves + wave) * 64 + lane);
             offB[i] = (uint32_t)(((q / CPR_B) * N + (q % CPR_B) * 8) * 2);
         }
-        // A fragment of tile tm, k-step ks: row waveM*WM + 32 tm + lane%32,
-        // logical chunk 2 ks + lane/32.
+        // A fragment of tile tm, k-step ks: row waveM*WM + 16 tm + lane%16,
+        // logical chunk 4 ks + lane/16 (k = 32 ks + 8 (lane/16) .. +7).
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                rdA[tm][ks] = swizzleA((waveM * WM + tm * kMfmaM + lane % 32) * CPR_A + 2 * ks + lane / 32) * 16;
+                rdA[tm][ks] = swizzleA((waveM * WM + tm * kMfmaM + lane % 16) * CPR_A + 4 * ks + lane / 16) * 16;
         // B fragment of tile tn: 16-lane group g = lane/16, s = lane%16 reads row
-        // 8 (g/2) + s/4 (+16 ks + 4 h), columns waveN*WN + 32 tn + 16 (g%2) + 4 (s%4).
-        // Rows enter the swizzle only through row % 4 = s/4, so k-step and half
-        // offsets stay outside the XOR as compile-time immediates.
+        // 8 g + s/4 (+32 ks + 4 h), columns waveN*WN + 16 tn + 4 (s%4). The
+        // swizzle sees rows only through bits 0, 1 and 3, all set per lane here,
+        // so k-step and half offsets stay outside the XOR as compile-time
+        // immediates.
         {
             const int g = lane / 16;
             const int s = lane % 16;
-            const int rowLane = 8 * (g / 2) + s / 4;
+            const int rowLane = 8 * g + s / 4;
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
-                const int col = waveN * WN + tn * kMfmaN + 16 * (g % 2) + 4 * (s % 4);
+                const int col = waveN * WN + tn * kMfmaN + 4 * (s % 4);
                 rdB[tn] = T::kRegionA + swizzleB<CPR_B>(rowLane * CPR_B + col / 8) * 16 + (col % 8) * 2;
             }
         }
@@ -282,7 +292,7 @@ struct GemmBlock {
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) acc[tm][tn][e] = 0.0f;
+                for (int e = 0; e < 4; ++e) acc[tm][tn][e] = 0.0f;
     }
 
     // Refills LDS stage `stage` with K tile kTile (this wave's share). No vector
@@ -323,7 +333,7 @@ struct GemmBlock {
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
-                acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
+                acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
     }
 
     // FP32 -> FP16 (nearest even), 8-byte stores of four consecutive columns,
@@ -331,22 +341,18 @@ struct GemmBlock {
     __device__ __forceinline__ void store(_Float16* C, int N) const {
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
-            const int m = blockRow + waveM * WM + tm * kMfmaM + lane % 32;
-            _Float16* crow = C + (size_t)m * N;
+            const int m = blockRow + waveM * WM + tm * kMfmaM + lane % 16;
+            _Float16* crow = C + (size_t)m * N + blockCol + waveN * WN + 4 * (lane / 16);
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
-                const int n0 = blockCol + waveN * WN + tn * kMfmaN + 4 * (lane / 32);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    half4_t v;
-                    v[0] = (_Float16)acc[tm][tn][4 * i + 0];
-                    v[1] = (_Float16)acc[tm][tn][4 * i + 1];
-                    v[2] = (_Float16)acc[tm][tn][4 * i + 2];
-                    v[3] = (_Float16)acc[tm][tn][4 * i + 3];
-                    *(half4_t*)(crow + n0 + 8 * i) = v;
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                half4_t v;
+                v[0] = (_Float16)acc[tm][tn][0];
+                v[1] = (_Float16)acc[tm][tn][1];
+                v[2] = (_Float16)acc[tm][tn][2];
+                v[3] = (_Float16)acc[tm][tn][3];
+                *(half4_t*)(crow + tn * kMfmaN) = v;
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 };
@@ -405,15 +411,21 @@ void gemmMfmaKernel(const _Float16* __restrict__ A, const _Float16* __restrict__
     half8_t fb[2][TN];
     blk.template readFrags<0>(0, fa[0], fb[0]);
 
-    for (int kt0 = 0; kt0 < numK; kt0 += STAGES) {
-        staticFor<STAGES>([&](auto sC) {
-            constexpr int s = sC.value;
+    // Fragment buffers alternate per k-step across tile boundaries. One pass of
+    // the loop covers U tiles, a whole number of ring turns with an even number
+    // of k-steps, so every buffer index and stage number is a compile-time
+    // constant.
+    constexpr int U = (STAGES * KS) % 2 == 0 ? STAGES : 2 * STAGES;
+    for (int kt0 = 0; kt0 < numK; kt0 += U) {
+        staticFor<U>([&](auto iC) {
+            constexpr int i = iC.value;
+            constexpr int s = i % STAGES;
             constexpr int sNext = (s + 1) % STAGES;
-            const int kt = kt0 + s;
+            const int kt = kt0 + i;
             if (kt < numK) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    const int cur = ks & 1;
+                    const int cur = (i * KS + ks) & 1;
                     if (ks + 1 < KS) {
                         blk.template readFrags<s>(ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
                     } else if (kt + 1 < numK) {
