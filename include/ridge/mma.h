@@ -1,6 +1,6 @@
 // ridge/mma.h -- the matrix instruction shape for a dtype on a target.
 // Counterpart of include/ridge/mma.h:7-13 of the reference, now taken from the
-// hardware model (m16n8k16 on sm_80, v_mfma_f32_32x32x16_f16 on gfx950).
+// hardware model (m16n8k16 on sm_80, v_mfma_f32_16x16x32_f16 on gfx950).
 #pragma once
 #include <cstdint>
 #include "ridge/config.h"

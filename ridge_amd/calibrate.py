@@ -45,7 +45,7 @@ def detect_arch(text):
 def parse_results(text):
     out = {}
     for line in text.splitlines():
-        m = re.match(r"CAL_RESULT\s+(\S+)\s+(\S+)", line)
+        m = re.match(r"CAL_(?:RESULT|INFO)\s+(\S+)\s+(\S+)", line)
         if m:
             out[m.group(1)] = float(m.group(2))
     return out
@@ -105,9 +105,9 @@ def hardware_json(res, spec, arch):
         "maxCtasPerSM": 32,
         "warpsNeededToHide": res["warpsNeededToHide"],
         "waveSize": 64,
-        "mmaM": 32,
-        "mmaN": 32,
-        "mmaK": 16,
+        "mmaM": 16,
+        "mmaN": 16,
+        "mmaK": 32,
         "simdsPerSM": 4,
         "regsPerSimdLane": 512,
         "regGranule": 8,
@@ -120,6 +120,8 @@ def hardware_json(res, spec, arch):
         "ldsControlBytesPerCycle": res["ldsControlBytesPerCycle"],
         "ldsAReadBytesPerCycle": res.get("ldsAReadBytesPerCycle", 0.0),
         "ldsBTrReadBytesPerCycle": res.get("ldsBTrReadBytesPerCycle", 0.0),
+        "mfma32x32x16CyclesPerInst": res.get("mfma32x32x16CyclesPerInst", 0.0),
+        "mfma32x32x16ClockHz": res.get("mfma32x32x16ClockHz", 0.0),
     }
 
 

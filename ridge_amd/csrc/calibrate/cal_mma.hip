@@ -1,4 +1,5 @@
-// cal_mma.hip -- mmaCyclesPerInst: CU-level cycles per v_mfma_f32_32x32x16_f16.
+// cal_mma.hip -- mmaCyclesPerInst: CU-level cycles per v_mfma_f32_16x16x32_f16,
+// the instruction the GEMM kernels issue.
 //
 // Counterpart of the reference's bench/calibrate/cal-mma.cu:41-163. The trap is
 // the same: throughput, not latency. Each wave keeps kIlp independent accumulator
@@ -7,8 +8,16 @@
 // swept (one workgroup per CU) because "CU-level" only means something once all
 // four SIMDs are busy: one wave drives one SIMD, four waves saturate the CU.
 //
+// Operands are the GEMM's: random U[-1,1) halves, a different fragment pair on
+// every instruction (eight of each, rotated). MI355X is power-limited under a
+// full-chip matrix load, and the loaded clock depends on how many operand bits
+// toggle: constant operands run hundreds of MHz faster than GEMM data, so a
+// constant-operand clock would overstate every prediction. The 32x32x16 form is
+// timed the same way at saturation for comparison (it issues the same FLOP per
+// cycle but draws more power, so its loaded clock is lower).
+//
 //   mmaCyclesPerInst  = median cycles / MFMAs issued on the CU
-//   impliedPeakTflops = 32768 / mmaCyclesPerInst * measured clock * CUs
+//   impliedPeakTflops = 16384 / mmaCyclesPerInst * measured clock * CUs
 #include "cal_common.hpp"
 
 using namespace ridgecal;
@@ -16,60 +25,117 @@ using namespace ridgecal;
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kIlp = 4;
-constexpr int kIters = 4000;
-constexpr double kMfmaFlops = 32768.0;
+constexpr int kIlp = 8;          // independent accumulators per wave
+constexpr int kFrags = 8;        // distinct operand fragments rotated through
+constexpr int kIters = 2000;     // x kIlp x 4 MFMAs per wave
+constexpr int kInner = 4;
+constexpr double kMfmaFlops = 16384.0;
+constexpr double kMfma32Flops = 32768.0;
 
-template <int Waves>
-__global__ __launch_bounds__(Waves * 64) void mfmaThroughputKernel(int iters, float* sink, Stamp* out) {
+// kFrags fragments of 8 halves per lane for A and for B: 2 x 8 x 64 x 16 bytes.
+constexpr int kOperandHalves = 2 * kFrags * 64 * 8;
+
+// Shape 0: v_mfma_f32_16x16x32_f16 (4 accumulator registers). Shape 1:
+// v_mfma_f32_32x32x16_f16 (16), issued half as often for the same FLOP.
+template <int Waves, int Shape>
+__global__ __launch_bounds__(Waves * 64) void mfmaThroughputKernel(const half8_t* __restrict__ operands, int iters,
+                                                                   float* sink, Stamp* out) {
     extern __shared__ char lds[];  // requested only to force one workgroup per CU
     const int lane = threadIdx.x % 64;
-    half8_t a, b;
+    half8_t a[kFrags], b[kFrags];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        // Finite values near 1, perturbed per lane so nothing constant-folds.
-        a[i] = (_Float16)(1.0f + 0.001f * float((lane + i) & 15));
-        b[i] = (_Float16)(1.0f - 0.001f * float((lane * 3 + i) & 15));
+    for (int f = 0; f < kFrags; ++f) {
+        a[f] = operands[f * 64 + lane];
+        b[f] = operands[(kFrags + f) * 64 + lane];
     }
-    float16_t acc[kIlp];
-#pragma unroll
-    for (int j = 0; j < kIlp; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[j][e] = float(threadIdx.x) * 1e-6f;
     if (threadIdx.x == 0) lds[0] = 0;
     __syncthreads();
-    const uint64_t c0 = cycles();
-    const uint64_t r0 = realtime();
-    for (int i = 0; i < iters; ++i) {
-#pragma unroll
-        for (int j = 0; j < kIlp; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
-    }
-    __syncthreads();
-    const uint64_t c1 = cycles();
-    const uint64_t r1 = realtime();
+    uint64_t c0, c1, r0, r1;
     float s = 0.0f;
+    if constexpr (Shape == 0) {
+        float4_t acc[kIlp];
 #pragma unroll
-    for (int j = 0; j < kIlp; ++j)
+        for (int j = 0; j < kIlp; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s += acc[j][e];
+            for (int e = 0; e < 4; ++e) acc[j][e] = 0.0f;
+        c0 = cycles();
+        r0 = realtime();
+        for (int i = 0; i < iters; ++i) {
+#pragma unroll
+            for (int u = 0; u < kInner; ++u)
+#pragma unroll
+                for (int j = 0; j < kIlp; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[(j + u) % kFrags], b[(3 * j + u) % kFrags],
+                                                                    acc[j], 0, 0, 0);
+        }
+        __syncthreads();
+        c1 = cycles();
+        r1 = realtime();
+#pragma unroll
+        for (int j = 0; j < kIlp; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s += acc[j][e];
+    } else {
+        float16_t acc[kIlp / 2];
+#pragma unroll
+        for (int j = 0; j < kIlp / 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+        c0 = cycles();
+        r0 = realtime();
+        for (int i = 0; i < iters; ++i) {
+#pragma unroll
+            for (int u = 0; u < kInner; ++u)
+#pragma unroll
+                for (int j = 0; j < kIlp / 2; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[(j + u) % kFrags], b[(3 * j + u) % kFrags],
+                                                                    acc[j], 0, 0, 0);
+        }
+        __syncthreads();
+        c1 = cycles();
+        r1 = realtime();
+#pragma unroll
+        for (int j = 0; j < kIlp / 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s += acc[j][e];
+    }
     if (s == 1.2345678e30f) sink[0] = s;
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
 }
 
-template <int Waves>
-void measure(int cus, float* dSink, Stamp* dStamps, double& cyclesPerMfma, double& clockHz) {
-    auto k = mfmaThroughputKernel<Waves>;
+// Median cycles per MFMA on one CU (Waves waves issuing) and the loaded clock.
+template <int Waves, int Shape>
+void measure(int cus, const half8_t* dOperands, float* dSink, Stamp* dStamps, double& cyclesPerMfma,
+             double& clockHz) {
+    auto k = mfmaThroughputKernel<Waves, Shape>;
     CAL_HIP_CHECK(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kOneWorkgroupLds));
-    hipLaunchKernelGGL(k, dim3(cus), dim3(Waves * 64), kOneWorkgroupLds, nullptr, kIters, dSink, dStamps);
+    hipLaunchKernelGGL(k, dim3(cus), dim3(Waves * 64), kOneWorkgroupLds, nullptr, dOperands, kIters, dSink, dStamps);
     CAL_HIP_CHECK(hipGetLastError());
     CAL_HIP_CHECK(hipDeviceSynchronize());
     std::vector<Stamp> st(cus);
     CAL_HIP_CHECK(hipMemcpy(st.data(), dStamps, cus * sizeof(Stamp), hipMemcpyDeviceToHost));
     double cyc = 0.0;
     medianStamps(st, cyc, clockHz);
-    cyclesPerMfma = cyc / (double(Waves) * kIters * kIlp);
+    const int perIter = kInner * (Shape == 0 ? kIlp : kIlp / 2);
+    cyclesPerMfma = cyc / (double(Waves) * kIters * perIter);
+}
+
+// U[-1,1) halves from splitmix64, the distribution the GEMM inputs are drawn from.
+std::vector<_Float16> randomOperands() {
+    std::vector<_Float16> h(kOperandHalves);
+    uint64_t state = 0x5eedULL;
+    for (auto& x : h) {
+        state += 0x9e3779b97f4a7c15ULL;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+        z ^= z >> 31;
+        x = (_Float16)(float(z >> 40) * (1.0f / 8388608.0f) - 1.0f);
+    }
+    return h;
 }
 
 }  // namespace
@@ -79,12 +145,16 @@ int main() {
     const int cus = prop.multiProcessorCount;
     float* dSink = nullptr;
     Stamp* dStamps = nullptr;
+    half8_t* dOperands = nullptr;
     CAL_HIP_CHECK(hipMalloc(&dSink, sizeof(float)));
     CAL_HIP_CHECK(hipMalloc(&dStamps, cus * sizeof(Stamp)));
+    CAL_HIP_CHECK(hipMalloc(&dOperands, kOperandHalves * sizeof(_Float16)));
+    const std::vector<_Float16> hOperands = randomOperands();
+    CAL_HIP_CHECK(hipMemcpy(dOperands, hOperands.data(), kOperandHalves * sizeof(_Float16), hipMemcpyHostToDevice));
     warmUp();
 
-    std::printf("\nv_mfma_f32_32x32x16_f16 issue rate, %d independent chains per wave, %d iterations\n", kIlp,
-                kIters);
+    std::printf("\nv_mfma_f32_16x16x32_f16 issue rate, %d independent chains per wave, %d fragments of random "
+                "U[-1,1) operands rotated, every CU\n", kIlp, kFrags);
     std::printf("  %6s %16s %14s %18s\n", "waves", "cycles/MFMA/CU", "clock MHz", "implied TFLOP/s");
     double best = 1e30, bestClock = 0.0;
     int bestWaves = 0;
@@ -94,7 +164,7 @@ int main() {
         std::vector<double> reps, clocks;                                                    \
         for (int r = 0; r < kRepeats; ++r) {                                                 \
             double c = 0, hz = 0;                                                            \
-            measure<W>(cus, dSink, dStamps, c, hz);                                          \
+            measure<W, 0>(cus, dOperands, dSink, dStamps, c, hz);                            \
             reps.push_back(c);                                                               \
             clocks.push_back(hz);                                                            \
         }                                                                                    \
@@ -115,6 +185,20 @@ int main() {
     CAL_SWEEP(16);
 #undef CAL_SWEEP
 
+    // The 32x32x16 form at the same saturation, for comparison.
+    std::vector<double> reps32, clocks32;
+    for (int r = 0; r < kRepeats; ++r) {
+        double c = 0, hz = 0;
+        measure<4, 1>(cus, dOperands, dSink, dStamps, c, hz);
+        reps32.push_back(c);
+        clocks32.push_back(hz);
+    }
+    const double c32 = median(reps32), hz32 = median(clocks32);
+    std::printf("\nv_mfma_f32_32x32x16_f16 at 4 waves per CU, same operands: %.4f cycles/MFMA/CU, %.1f MHz, "
+                "%.1f TFLOP/s\n", c32, hz32 / 1e6, kMfma32Flops / c32 * hz32 * cus / 1e12);
+    std::printf("CAL_INFO mfma32x32x16CyclesPerInst %.6f\n", c32);
+    std::printf("CAL_INFO mfma32x32x16ClockHz %.6e\n", hz32);
+
     const double peak = kMfmaFlops / best * bestClock * cus / 1e12;
     const double peakNominal = kMfmaFlops / best * (prop.clockRate * 1e3) * cus / 1e12;
     std::printf("\nsaturated at %d waves per CU\n", bestWaves);
@@ -131,5 +215,6 @@ int main() {
     std::printf("CAL_RESULT nominalClockHz %.6e\n", prop.clockRate * 1e3);
     CAL_HIP_CHECK(hipFree(dSink));
     CAL_HIP_CHECK(hipFree(dStamps));
+    CAL_HIP_CHECK(hipFree(dOperands));
     return stable ? 0 : 1;
 }

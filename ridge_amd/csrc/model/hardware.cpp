@@ -33,9 +33,9 @@ HardwareModel HardwareModel::a100() {
 HardwareModel HardwareModel::mi355x() {
     // Datasheet-derived placeholders for MI355X (gfx950):
     //   256 CUs (8 XCDs x 32) at a 2.4 GHz peak engine clock;
-    //   v_mfma_f32_32x32x16_f16 = 32768 FLOP, one per SIMD per 32 cycles, four
-    //     SIMDs per CU -> 8 CU-level cycles per instruction, i.e.
-    //     32768 / 8 * 2.4e9 * 256 = 2516.6 TFLOP/s dense FP16;
+    //   v_mfma_f32_16x16x32_f16 = 16384 FLOP, one per SIMD per 16 cycles, four
+    //     SIMDs per CU -> 4 CU-level cycles per instruction, i.e.
+    //     16384 / 4 * 2.4e9 * 256 = 2516.6 TFLOP/s dense FP16;
     //   LDS 160 KiB per CU, 128 bytes per cycle (placeholder until measured);
     //   HBM3E 8.0 TB/s;
     //   4 SIMDs x 512 VGPR+AGPR per lane x 64 lanes = 131072 lane-registers per CU,
@@ -44,7 +44,7 @@ HardwareModel HardwareModel::mi355x() {
     h.name = "MI355X (datasheet placeholders, replace with calibration)";
     h.numSMs = 256;
     h.clockHz = 2.4e9;
-    h.mmaCyclesPerInst = 8.0;
+    h.mmaCyclesPerInst = 4.0;
     h.smemBytesPerCycle = 128.0;
     h.hbmBytesPerSec = 8.0e12;
     h.regsPerSM = 131072;
@@ -55,9 +55,9 @@ HardwareModel HardwareModel::mi355x() {
     h.calibrated = false;
     h.arch = "gfx950";
     h.waveSize = 64;
-    h.mmaM = 32;
-    h.mmaN = 32;
-    h.mmaK = 16;
+    h.mmaM = 16;
+    h.mmaN = 16;
+    h.mmaK = 32;
     h.simdsPerSM = 4;
     h.regsPerSimdLane = 512;
     h.regGranule = 8;

@@ -8,7 +8,15 @@
 // a drift above 5% fails the run; a variant that cannot be measured is a failure,
 // not a silent skip.
 //
-//   ridge-measure [sweep.csv] [out.csv] [--allow-skip] [--warmup-seconds S]
+//   ridge-measure [sweep.csv] [out.csv] [--allow-skip] [--warmup-seconds S] [--settle-seconds T]
+//
+// --settle-seconds (default 0.2): every timed measurement -- each variant, each
+// hipBLASLt comparator and each canary -- first runs its own workload untimed for
+// T seconds. The reference locks the SM clock (setup-box.sh); MI355X clocks
+// cannot be locked and follow the power drawn by the current workload, so
+// without a settle a short measurement partly runs at the previous workload's
+// clock (unsettled 4096^3 canaries spread 6.1% over one sweep, with no trend).
+// The settle makes every figure a steady-state figure for its own work.
 //
 // --allow-skip: variants that do not divide a shape are recorded as skipped
 // instead of failing (for shapes such as N = 128 that only some tiles divide).
@@ -79,10 +87,12 @@ int main(int argc, char** argv) {
     std::vector<std::string> pos;
     bool allowSkip = false;
     double warmSeconds = 5.0;
+    double settleSeconds = 0.2;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if (a == "--allow-skip") allowSkip = true;
         else if (a == "--warmup-seconds" && i + 1 < argc) warmSeconds = std::atof(argv[++i]);
+        else if (a == "--settle-seconds" && i + 1 < argc) settleSeconds = std::atof(argv[++i]);
         else pos.push_back(a);
     }
     const std::string sweepPath = pos.size() > 0 ? pos[0] : "data/sweep/mi355x-registered.csv";
@@ -132,8 +142,10 @@ int main(int argc, char** argv) {
     blas.prepare(dA, dB, dC, 4096, 4096, 4096);
     std::printf("warmup %.0fs\n", warmSeconds);
     warmUp([&] { blas.gemm(dA, dB, dC, 4096, 4096, 4096); }, warmSeconds);
+    auto canaryBody = [&] { blas.gemm(dA, dB, dC, 4096, 4096, 4096); };
     auto measureCanary = [&] {
-        return timeTflops([&] { blas.gemm(dA, dB, dC, 4096, 4096, 4096); }, canaryFlops).tflops;
+        warmUp(canaryBody, settleSeconds);
+        return timeTflops(canaryBody, canaryFlops).tflops;
     };
     const double canaryFirst = measureCanary();
     double canaryNow = canaryFirst, canaryMin = canaryFirst, canaryMax = canaryFirst;
@@ -151,6 +163,7 @@ int main(int argc, char** argv) {
         << "# kernel_library," << ridge_gemm_build_info() << "\n"
         << "# inputs,U[-1;1) fp16 splitmix64 seeds 1 and 2\n"
         << "# warmup_seconds," << warmSeconds << "\n"
+        << "# settle_seconds," << settleSeconds << "\n"
         << "# canary_start_tflops," << canaryFirst << "\n"
         << "M,N,K,tag,BM,BN,BK,WM,WN,stages,groupM,regsPerThread,smemBytes,threads,"
            "tflops,blas_tflops,fraction_of_blas,canary_tflops,ms,iters\n";
@@ -160,7 +173,9 @@ int main(int argc, char** argv) {
     for (const Shape& s : shapes) {
         const double flops = 2.0 * s.M * s.N * s.K;
         blas.prepare(dA, dB, dC, s.M, s.N, s.K);
-        const double blasTflops = timeTflops([&] { blas.gemm(dA, dB, dC, s.M, s.N, s.K); }, flops).tflops;
+        auto blasBody = [&] { blas.gemm(dA, dB, dC, s.M, s.N, s.K); };
+        warmUp(blasBody, settleSeconds);
+        const double blasTflops = timeTflops(blasBody, flops).tflops;
         std::printf("%5dx%5dx%5d  %-24s  hipBLASLt %8.2f TFLOP/s\n", s.M, s.N, s.K, s.tag.c_str(), blasTflops);
         std::fflush(stdout);
         for (int v = 0; v < nv; ++v) {
@@ -177,7 +192,9 @@ int main(int argc, char** argv) {
                 ++failed;
                 continue;
             }
-            const Timing t = timeTflops([&] { ridge_gemm_launch(v, dA, dB, dC, s.M, s.N, s.K, nullptr); }, flops);
+            auto body = [&] { ridge_gemm_launch(v, dA, dB, dC, s.M, s.N, s.K, nullptr); };
+            warmUp(body, settleSeconds);
+            const Timing t = timeTflops(body, flops);
             if (++measurements % kCanaryEvery == 0) {
                 canaryNow = measureCanary();
                 canaryMin = std::min(canaryMin, canaryNow);

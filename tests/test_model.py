@@ -112,8 +112,8 @@ def test_mi355x_worked_example(mi355x):
     the MI355X placeholders. Derivation:
 
       waves          (256/128) x (256/64) = 8, 512 workitems
-      MFMA/wave/step (128/32) x (64/32) x (64/16) = 32
-      tCompute       32 x 8 waves x 8 cycles = 2048
+      MFMA/wave/step (128/16) x (64/16) x (64/32) = 64
+      tCompute       64 x 8 waves x 4 cycles = 2048
       tSmem          8 x (128 + 64) x 64 x 2 B = 196608 B / 128 = 1536
       tStep          3584, smEff 2048/3584 = 0.571429
       LDS            2 x (256x64 + 64x256) x 2 = 131072 -> floor(163840/131072) = 1
@@ -127,7 +127,7 @@ def test_mi355x_worked_example(mi355x):
       epilogue       256 x 256 x 2 / 13.0208333 = 10066.3296
       body           64 K-steps x 3584 = 229376
       envelope       229376 / 244475.4944 = 0.938237
-      peak           32768 / 8 x 2.4e9 x 256 = 2516.5824 TFLOP/s
+      peak           16384 / 4 x 2.4e9 x 256 = 2516.5824 TFLOP/s
       compute        2516.5824 x 0.571429 x 0.938237 = 1349.22
       base AI        2 x 256 x 256 x 4096 / ((256 + 256) x 4096 x 2) = 128
       per-XCD block  32 slots per XCD: a = floor(sqrt 32) = 5, b = ceil(32/5) = 7,
