@@ -18,7 +18,13 @@ same way. Prints ONE JSON line.
 cpu_baseline: the CPU f64 GEMM of the oracle (a port of the reference's CPU
 reference, bench/check-gemm.cu:98-108, row-parallel with OpenMP) timed on a
 bounded sample of the same 4096^3 workload (a block of output rows, about 10 s of
-work), reported in TFLOP/s with the thread count used.
+work), reported in TFLOP/s with the thread count used (the cores this process may
+run on, at most 16).
+
+autotune: the metric's second half, the mean top-10 regret of the model-pruned
+autotuner, is computed from the committed measured sweep (data/measured/mi355x.csv,
+14 shapes x 24 variants) and the committed calibration (data/hardware/mi355x.json)
+by ridge_amd.autotune; it is a property of the sweep, not of this run's timing.
 """
 
 import argparse
@@ -36,7 +42,12 @@ PEAK_HBM_GBS = 8000.0
 DEFAULT_SHAPE = (4096, 4096, 4096)
 # The registered variant the sweep measured fastest at 4096^3.
 DEFAULT_VARIANT = (256, 256, 32, 128, 64, 4, 4)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemmMfmaPingPong_256x256x32w128x64s4g4_4096cube_traffic.json")
+PROFILES = os.path.join(ROOT, "profiles")
+MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x.csv")
+HARDWARE_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+# Host threads for the CPU baseline: the cores this process may use, capped at
+# the 16 a GPU box grants one GPU.
+MAX_CPU_THREADS = 16
 
 
 def parse_ints(s, n):
@@ -63,6 +74,60 @@ def time_launches(fn, steps, stream):
     return wall, e0.elapsed_time(e1)
 
 
+def roofline(M, N, K, per_launch_ms, traffic):
+    """The bound the shape's arithmetic intensity puts it under (datasheet ridge
+    point 2516.6 / 8 = 315 FLOP/B) and the algorithmic rate against it: FLOP/s for
+    MFMA-bound shapes, compulsory bytes 2(MK + KN + MN) per second for HBM-bound
+    ones, from the HIP-event time per launch."""
+    flops = 2.0 * M * N * K
+    nbytes = 2.0 * (M * K + K * N + M * N)
+    sec = per_launch_ms * 1e-3
+    if flops / nbytes >= PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
+        achieved = flops / sec / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic}
+    achieved = nbytes / sec / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic}
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, MAX_CPU_THREADS))
+
+
+def measured_traffic(M, N, K, key):
+    """HBM bytes per launch from the committed rocprofv3 traffic summary for this
+    shape and variant, or None when no profile covers it."""
+    if not os.path.isdir(PROFILES):
+        return None
+    for name in sorted(os.listdir(PROFILES)):
+        if not name.endswith("_traffic.json"):
+            continue
+        with open(os.path.join(PROFILES, name)) as f:
+            t = json.load(f)
+        if tuple(t.get("shape", ())) == (M, N, K) and tuple(t.get("variant", ())) == key:
+            return t.get("hbm_bytes_per_launch")
+    return None
+
+
+def autotune_regret(k=10):
+    """Mean and max regret at top-k over the committed sweep, or None if the model
+    CLI is not built."""
+    try:
+        from ridge_amd import autotune as AT
+        table, total, shapes, _ = AT.evaluate(MEASURED_SWEEP, HARDWARE_JSON, ks=(k,))
+    except Exception as e:  # the model CLI is part of the build; report its absence
+        return {"error": "%s" % e}
+    row = table[0]
+    return {"top_k": k, "mean_regret_pct": round(row["mean_regret"], 3), "max_regret_pct": round(row["max_regret"], 3),
+            "exact_hits": row["hits"], "shapes": shapes, "configs": total,
+            "benchmarks_vs_exhaustive": round(row["reduction"], 2), "source": "data/measured/mi355x.csv"}
+
+
 def cpu_baseline(M, N, K, seconds=10.0):
     """f64 oracle GEMM on a block of output rows of the same workload."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -70,7 +135,7 @@ def cpu_baseline(M, N, K, seconds=10.0):
     import oracle as O
     Ab = O.uniform_fill_f16(M * K, 1).reshape(M, K)
     Bb = O.uniform_fill_f16(K * N, 2)
-    threads = os.cpu_count() or 1
+    threads = cpu_threads()
     # Grow the row block until one call takes about `seconds` (each call also
     # pays the one-off conversion of B, which the first small blocks are
     # dominated by, so the estimate is refined from the previous call).
@@ -199,22 +264,17 @@ def main():
     wall, ev_ms = time_launches(step, args.steps, stream)
     value = flops * args.steps / wall / 1e12
     per_launch_ms = ev_ms / args.steps
-    achieved = flops / (per_launch_ms * 1e-3) / 1e12
 
     if blas is not None:
         _, ms = time_launches(blas_step, args.steps, stream)
         blas_after = flops * args.steps / (ms * 1e-3) / 1e12
         blas.close()
 
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-        if tuple(t.get("shape", ())) == (M, N, K) and tuple(t.get("variant", ())) == key:
-            traffic = t.get("hbm_bytes_per_launch")
+    traffic = measured_traffic(M, N, K, key)
 
     out = {
-        "metric": "FP16 GEMM TFLOP/s @4096^3 on 1 MI355X (% MFMA peak, % hipBLASLt); top-10 regret",
+        "metric": "FP16 GEMM TFLOP/s @4096^3 on 1 MI355X (% MFMA peak, % hipBLASLt); top-10 regret"
+                  if (M, N, K) == DEFAULT_SHAPE else "FP16 GEMM TFLOP/s @%dx%dx%d on 1 MI355X" % (M, N, K),
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -229,8 +289,7 @@ def main():
         "config": {"workload": "FP16 GEMM M=%d N=%d K=%d, row-major A/B/C, FP32 accumulate, FP16 C" % (M, N, K),
                    "variant": v.label(), "parallelism": "single GPU"},
         "frac_of_mfma_peak": round(value / PEAK_FP16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic},
+        "roofline": roofline(M, N, K, per_launch_ms, traffic),
     }
     if blas_before is not None:
         best = max(blas_before, blas_after)
@@ -238,6 +297,7 @@ def main():
                             "after": round(blas_after, 3),
                             "drift": round(abs(blas_after - blas_before) / blas_before, 4),
                             "frac_of_hipblaslt": round(value / best, 4)}
+    out["autotune"] = autotune_regret(10)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)
         out["cpu_baseline_naive_1core"] = cpu_baseline_naive_1core()
