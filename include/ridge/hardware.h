@@ -29,6 +29,8 @@ struct HardwareModel {
     int maxCtasPerSM = 0;            // resident workgroups per SM/CU
 
     double warpsNeededToHide = 0.0;  // [CAL] resident warps/waves that hide latency
+    double warpsNeededToHideIlp8 = 0.0;  // [CAL] the same with 8 independent chains per
+                                         // wave; 0 = not measured (reference: unused)
 
     bool calibrated = false;         // every [CAL] constant came from a measurement
 
@@ -44,6 +46,11 @@ struct HardwareModel {
     int cBytes = 4;                  // bytes per output element drained by the epilogue
     int l2ReuseModel = 0;            // 0: sqrt(ctaSlots) square reuse (reference)
                                      // 1: per-XCD resident block, bounded by the grid
+    int prologueModel = 0;           // 0: the prologue always fills stages-1 tiles (reference)
+                                     // 1: only the K tiles that exist, min(stages-1, K/BK)
+    int pingPongModel = 0;           // 0: operand reads in series with the MFMAs (reference)
+                                     // 1: a workgroup of 2 waves per SIMD with >= 3 stages runs
+                                     //    the ping-pong schedule: reads overlap the MFMAs
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -1,6 +1,7 @@
 """Runs the four calibration microbenchmarks and writes the hardware JSON.
 
     python -m ridge_amd.calibrate [--binary-dir ridge_amd/bin] [--out data/hardware/mi355x.json] [--check]
+    python -m ridge_amd.calibrate --from-log data/hardware/mi355x-calibration.txt   # re-derive, no GPU
 
 Counterpart of the reference's bench/calibrate/run-calibration.py:29-159. The
 constants come from the benchmarks; the datasheet figures below are independent
@@ -43,11 +44,18 @@ def detect_arch(text):
 
 
 def parse_results(text):
+    """CAL_RESULT / CAL_INFO key-value lines, plus each column of the latency
+    surface's saturation (CAL_SATURATION ilp <k> waves <w>) as
+    warpsNeededToHideIlp<k>."""
     out = {}
     for line in text.splitlines():
         m = re.match(r"CAL_(?:RESULT|INFO)\s+(\S+)\s+(\S+)", line)
         if m:
             out[m.group(1)] = float(m.group(2))
+            continue
+        m = re.match(r"CAL_SATURATION\s+ilp\s+(\d+)\s+waves\s+(\d+)", line)
+        if m:
+            out["warpsNeededToHideIlp" + m.group(1)] = float(m.group(2))
     return out
 
 
@@ -114,6 +122,9 @@ def hardware_json(res, spec, arch):
         "numXcds": 8,
         "cBytes": 2,
         "l2ReuseModel": 1,
+        "prologueModel": 1,
+        "pingPongModel": 1,
+        "warpsNeededToHideIlp8": res.get("warpsNeededToHideIlp8", 0.0),
         "nominalClockHz": res.get("nominalClockHz", spec["clock_hz"]),
         "impliedPeakTflops": res["impliedPeakTflops"],
         "mallBytesPerSec": res.get("mallBytesPerSec", 0.0),
@@ -131,18 +142,25 @@ def main(argv=None):
     ap.add_argument("--out", default=os.path.join(ROOT, "data", "hardware", "mi355x.json"))
     ap.add_argument("--check", action="store_true", help="band-check only, write nothing")
     ap.add_argument("--log", default=None, help="also write the benchmarks' output here")
+    ap.add_argument("--from-log", default=None,
+                    help="derive the JSON from a saved benchmark log (a --log file) instead of running")
     args = ap.parse_args(argv)
 
     results, banner, failed = {}, "", False
-    for name in BENCHMARKS:
-        res, out, rc = run_benchmark(args.binary_dir, name)
-        results.update(res)
-        banner += out
-        if rc != 0:
-            print("  %s exited %d: its constants are unstable" % (name, rc))
-            failed = True
-        print()
-    if args.log:
+    if args.from_log:
+        with open(args.from_log) as f:
+            banner = f.read()
+        results = parse_results(banner)
+    else:
+        for name in BENCHMARKS:
+            res, out, rc = run_benchmark(args.binary_dir, name)
+            results.update(res)
+            banner += out
+            if rc != 0:
+                print("  %s exited %d: its constants are unstable" % (name, rc))
+                failed = True
+            print()
+    if args.log and not args.from_log:
         with open(args.log, "w") as f:
             f.write(banner)
 

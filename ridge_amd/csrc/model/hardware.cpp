@@ -64,6 +64,8 @@ HardwareModel HardwareModel::mi355x() {
     h.numXcds = 8;
     h.cBytes = 2;
     h.l2ReuseModel = 1;
+    h.prologueModel = 1;
+    h.pingPongModel = 1;
     return h;
 }
 
@@ -170,6 +172,11 @@ bool optionalInteger(const std::map<std::string, std::string>& kv, const char* k
     return integer(kv, key, out, err);
 }
 
+bool optionalNumber(const std::map<std::string, std::string>& kv, const char* key, double& out, std::string& err) {
+    if (kv.find(key) == kv.end()) return true;
+    return number(kv, key, out, err);
+}
+
 }  // namespace
 
 bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, std::string& err) {
@@ -208,7 +215,10 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
         !optionalInteger(kv, "regsPerSimdLane", h.regsPerSimdLane, err) ||
         !optionalInteger(kv, "regGranule", h.regGranule, err) ||
         !optionalInteger(kv, "numXcds", h.numXcds, err) || !optionalInteger(kv, "cBytes", h.cBytes, err) ||
-        !optionalInteger(kv, "l2ReuseModel", h.l2ReuseModel, err)) {
+        !optionalInteger(kv, "l2ReuseModel", h.l2ReuseModel, err) ||
+        !optionalInteger(kv, "prologueModel", h.prologueModel, err) ||
+        !optionalInteger(kv, "pingPongModel", h.pingPongModel, err) ||
+        !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
         err = path + ": " + err;
         return false;
     }

@@ -17,6 +17,13 @@
 //                           the grid, and fetch their A and B panels once into
 //                           that XCD's L2; capped by the compulsory intensity of
 //                           the whole problem                 (reference :116-123)
+//   K-step time           = hw.pingPongModel 1: max(compute, operand reads) for a
+//                           workgroup of two waves per SIMD with >= 3 stages (the
+//                           ping-pong schedule), their sum otherwise (reference :47)
+//   prologue              = hw.prologueModel 1: min(stages-1, K/BK) tiles, the
+//                           tiles the kernel actually issues     (reference :91-98)
+//   latency hiding        = hw.warpsNeededToHideIlp8 when a wave carries >= 8
+//                           independent accumulator chains      (reference :72-74)
 //
 // With the defaults (a100() or a reference JSON) every term reduces to the
 // reference's expression in the same double-precision operation order, so the
@@ -101,7 +108,12 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const double tCompute = mmasPerWarpPerStep * numWarps * hw.mmaCyclesPerInst;
     const double smemBytesPerStep = double(numWarps) * (cfg.warpM + cfg.warpN) * cfg.BK * db;
     const double tSmem = smemBytesPerStep / hw.smemBytesPerCycle;
-    const double tStep = tCompute + tSmem;
+    // The ping-pong schedule (two waves per SIMD, a ring of three or more stages)
+    // runs one wave's operand reads under the other wave's MFMAs, so a K-step
+    // costs the longer of the two instead of their sum.
+    const bool pingPong = hw.pingPongModel == 1 && hw.simdsPerSM > 0 &&
+                          numWarps == 2 * hw.simdsPerSM && cfg.stages >= 3;
+    const double tStep = pingPong ? std::max(tCompute, tSmem) : tCompute + tSmem;
     const double smEfficiency = tCompute / tStep;
     p.tComputeCycles = tCompute;
     p.tSmemCycles = tSmem;
@@ -122,8 +134,15 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     }
     p.ctasPerSM = int(ctasPerSM);
 
+    // Latency hiding: resident waves against the calibrated need. A wave that
+    // carries 8 or more independent accumulator chains per K-step hides latency
+    // on its own ILP, and needs the ILP-8 column of the calibration surface
+    // (when measured) instead of the single-chain-pair default.
     const double activeWarps = ctasPerSM * numWarps;
-    const double occFactor = std::min(1.0, activeWarps / hw.warpsNeededToHide);
+    const double chains = double(cfg.warpM / cfg.mmaM) * (cfg.warpN / cfg.mmaN);
+    const double wavesToHide =
+        hw.warpsNeededToHideIlp8 > 0.0 && chains >= 8.0 ? hw.warpsNeededToHideIlp8 : hw.warpsNeededToHide;
+    const double occFactor = std::min(1.0, activeWarps / wavesToHide);
     p.occFactor = occFactor;
 
     // Wave quantisation over all resident workgroup slots.
@@ -143,7 +162,11 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const double gmemBytesPerCycle = hw.hbmBytesPerSec / (hw.clockHz * double(hw.numSMs));
     const double tileBytes = double(cfg.BM * cfg.BK + cfg.BK * cfg.BN) * db;
     const double kSteps = double(cfg.K) / cfg.BK;
-    const double tPrologue = double(cfg.stages - 1) * tileBytes / gmemBytesPerCycle / ctasPerSM;
+    // The reference fills stages-1 tiles whatever K is; the kernels here issue
+    // only the tiles that exist (prologueModel 1).
+    const double prologueTiles =
+        hw.prologueModel == 1 ? std::min(double(cfg.stages - 1), kSteps) : double(cfg.stages - 1);
+    const double tPrologue = prologueTiles * tileBytes / gmemBytesPerCycle / ctasPerSM;
     const double tEpilogue = double(cfg.BM) * cfg.BN * double(hw.cBytes) / gmemBytesPerCycle / ctasPerSM;
     const double tBody = kSteps * tStep;
     const double envelopeEfficiency = tBody / (tPrologue + tBody + tEpilogue);

@@ -156,6 +156,71 @@ def test_mi355x_worked_example(mi355x):
     assert p["bottleneck"] == "SMEM"
 
 
+def test_mi355x_ping_pong_overlap_and_prologue_of_existing_tiles(mi355x):
+    """256x256x32 tile, 128x64 wavefront tile, 4 stages, 197 registers on the
+    MI355X placeholders: 8 waves (two per SIMD) with >= 3 stages is the
+    ping-pong schedule, whose operand reads run under the other wave's MFMAs.
+
+      MFMA/wave/step (128/16) x (64/16) x (32/32) = 32
+      tCompute       32 x 8 waves x 4 cycles = 1024
+      tSmem          8 x (128 + 64) x 32 x 2 B = 98304 B / 128 = 768
+      tStep          max(1024, 768) = 1024 -> smEff 1 (in series: 1792, 0.571429)
+
+    At K = 64 only two K tiles exist: the prologue fills min(3, 2) = 2 of them,
+    2 x (256x32 + 32x256) x 2 B / 13.0208333 B/cycle = 5033.1648 cycles (the
+    reference's stages-1 rule would charge 3 tiles, 7549.7472)."""
+    p = RM.predict(mi355x, M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=4,
+                   regsPerThread=197)
+    assert p["tComputeCycles"] == pytest.approx(1024.0)
+    assert p["tSmemCycles"] == pytest.approx(768.0)
+    assert p["tStepCycles"] == pytest.approx(1024.0)
+    assert p["smEfficiency"] == pytest.approx(1.0)
+    # Two stages: the uniform schedule, reads and MFMAs in series.
+    p2 = RM.predict(mi355x, M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=2,
+                    regsPerThread=197)
+    assert p2["tStepCycles"] == pytest.approx(1792.0)
+    # Four waves: no ping-pong even with 4 stages.
+    p4 = RM.predict(mi355x, M=4096, N=4096, K=4096, BM=256, BN=128, BK=32, warpM=128, warpN=64, stages=4,
+                    regsPerThread=197)
+    # 32 MFMAs x 4 waves x 4 cycles + 4 x 192 x 32 x 2 B / 128 = 512 + 384.
+    assert p4["tStepCycles"] == pytest.approx(896.0)
+    short = RM.predict(mi355x, M=4096, N=4096, K=64, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=4,
+                       regsPerThread=197)
+    assert short["kSteps"] == 2
+    assert short["tPrologueCycles"] == pytest.approx(5033.1648, abs=1e-3)
+    ref = RM.predict(RM.Hardware("a100"), M=4096, N=4096, K=64, BM=256, BN=256, BK=32, warpM=64, warpN=64,
+                     stages=4, regsPerThread=0)
+    # A100 mode keeps the reference's rule: 3 tiles of (256x32 + 32x256) x 2 B at
+    # the a100() placeholder's 2.0e12 / (1.41e9 x 108) B/cycle.
+    gmem = 2.0e12 / (1.41e9 * 108)
+    assert ref["tPrologueCycles"] == pytest.approx(3 * 32768 / gmem / ref["ctasPerSM"], rel=1e-12)
+
+
+def test_mi355x_latency_hiding_uses_the_ilp8_column(tmp_path):
+    """A wave with >= 8 independent accumulator chains per K-step needs the ILP-8
+    column of the latency surface (4 waves here) instead of the default 8.
+    256x128 tile of 128x64 wavefront tiles: 4 waves of (128/16)(64/16) = 32
+    chains; 261 registers -> 264, floor(512/264) = 1 wave per SIMD -> 1 workgroup,
+    4 resident waves: occ 4/4 = 1 (default need: 4/8 = 0.5). 64x64 tile of 32x32
+    wavefront tiles: (32/16)(32/16) = 4 chains, so the default need of 8 holds."""
+    cfg = ('{"name": "x", "arch": "gfx950", "numSMs": 256, "clockHz": 2.4e9, "mmaCyclesPerInst": 4, '
+           '"smemBytesPerCycle": 128, "hbmBytesPerSec": 8e12, "regsPerSM": 131072, "smemBytesPerSM": 163840, '
+           '"maxWarpsPerSM": 32, "maxCtasPerSM": 32, "warpsNeededToHide": 8%s}')
+    with_ilp = tmp_path / "ilp.json"
+    with_ilp.write_text(cfg % ', "warpsNeededToHideIlp8": 4')
+    without = tmp_path / "no.json"
+    without.write_text(cfg % "")
+    big = dict(BM=256, BN=128, BK=32, warpM=128, warpN=64, stages=4, regsPerThread=261)
+    assert RM.predict(RM.Hardware(str(with_ilp)), **big)["occFactor"] == pytest.approx(1.0)
+    assert RM.predict(RM.Hardware(str(without)), **big)["occFactor"] == pytest.approx(0.5)
+    # 64x64 w32x32, 4 stages of 64x32 + 32x64 halves = 32 KiB: 5 by LDS, 8 by
+    # wave slots (32/4); 62 registers -> 64, 8 waves per SIMD -> 8 by registers;
+    # 5 workgroups x 4 waves = 20 resident waves >= 8 either way.
+    small = dict(BM=64, BN=64, BK=32, warpM=32, warpN=32, stages=4, regsPerThread=62)
+    p = RM.predict(RM.Hardware(str(with_ilp)), **small)
+    assert p["ctasPerSM"] == 5 and p["occFactor"] == pytest.approx(1.0)
+
+
 def test_mi355x_register_occupancy_per_simd(mi355x):
     # 4 waves of 133+128 = 261 registers: 264 rounded, floor(512/264) = 1 wave per
     # SIMD; 4 waves over 4 SIMDs = 1 per SIMD -> 1 workgroup. At 74 registers:
