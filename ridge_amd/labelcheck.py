@@ -1,0 +1,394 @@
+"""Cross-check of the cost model's bottleneck labels against rocprofv3 counters:
+the MI355X restatement of the reference's bench/run-ncu-validation.sh and its
+pre-registered decision table (data/sweep/ncu-label-mapping.md).
+
+    python -m ridge_amd.labelcheck select          # the registered config list
+    python -m ridge_amd.labelcheck run             # the launches, under rocprofv3
+    python -m ridge_amd.labelcheck gather --counters D1 --fetch D2 --write D3 --trace D4
+    python -m ridge_amd.labelcheck score           # the registered decision table
+
+The decision table, the counters, the config-selection rule and the pass
+criterion are fixed in data/sweep/rocprof-label-mapping.md and
+data/sweep/rocprof-label-configs.csv, both committed before the first run.
+`run` and `gather` only launch kernels and collect numbers; `score` applies the
+registered table and nothing else, so the rule cannot drift after the data
+exists (the reference's own discipline, run-ncu-validation.sh:1-6).
+
+`run` must be the program rocprofv3 starts (`rocprofv3 ... -- python3 -m
+ridge_amd.labelcheck run`). It launches, for every config in order, the
+registered variant LAUNCHES times on seeded U[-1,1) inputs; `gather` assigns the
+GEMM dispatches of each rocprofv3 pass to configs by dispatch order and checks
+every dispatch's kernel name against the config's template arguments.
+"""
+
+import argparse
+import csv
+import glob
+import json
+import os
+import re
+import statistics
+import sys
+
+from ridge_amd import model as RM
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HW_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+SOURCES = [os.path.join(ROOT, "data", "measured", "mi355x.csv"),
+           os.path.join(ROOT, "data", "measured", "mi355x-baseline-configs.csv")]
+CONFIGS_CSV = os.path.join(ROOT, "data", "sweep", "rocprof-label-configs.csv")
+COUNTERS_CSV = os.path.join(ROOT, "data", "measured", "rocprof-labels.csv")
+
+LAUNCHES = 3
+PER_LABEL = 4
+LABEL_ORDER = ["SMEM", "WAVES", "ENVELOPE", "OCC", "HBM", "TENSOR_CORE"]
+
+# Registered decision table (data/sweep/rocprof-label-mapping.md section 2),
+# applied top to bottom, first match wins.
+HBM_PCT_MIN = 70.0          # rule 1: HBM% >= 70            -> HBM
+SIMD_UTIL_PCT_MAX = 80.0    # rule 2: SIMD utilisation < 80 -> WAVES
+OCC_SHORTFALL_MAX = 0.70    # rule 3: achieved/theoretical waves < 0.70 -> OCC
+MFMA_PCT_MIN = 70.0         # rule 5: MFMA% >= 70           -> TENSOR_CORE
+PASS_FRACTION = 0.75        # pass: at least 75% of configs agree
+
+# Traffic scaling of FETCH_SIZE / WRITE_SIZE on this chip: a 256 MiB device
+# copy reads FETCH_SIZE 131,083.5 KiB and WRITE_SIZE 262,144 KiB.
+FETCH_SCALE = 2.000
+WRITE_SCALE = 1.000
+
+PASS1_COUNTERS = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_WAVE_CYCLES", "SQ_LDS_IDX_ACTIVE",
+                  "SQ_WAVES", "SQ_INSTS_MFMA", "GRBM_GUI_ACTIVE", "GRBM_COUNT"]
+
+KEY_FIELDS = ["BM", "BN", "BK", "WM", "WN", "stages", "groupM"]
+# 4096^3 with the bench's default variant.
+CONTROL = (4096, 4096, 4096, 256, 256, 32, 128, 64, 4, 4)
+CONTROL_SIMD_UTIL_PCT = (80.0, 105.0)
+
+
+def _read_rows(path):
+    with open(path) as f:
+        return list(csv.DictReader(line for line in f if not line.startswith("#")))
+
+
+def predict_row(hw, r):
+    return RM.predict(hw, M=int(r["M"]), N=int(r["N"]), K=int(r["K"]), BM=int(r["BM"]), BN=int(r["BN"]),
+                      BK=int(r["BK"]), warpM=int(r["WM"]), warpN=int(r["WN"]), stages=int(r["stages"]),
+                      regsPerThread=int(r["regsPerThread"]))
+
+
+def _config_row(label, r, p):
+    return {"predicted_label": label, "model_label": p["bottleneck"], "tag": r["tag"], "M": int(r["M"]),
+            "N": int(r["N"]), "K": int(r["K"]), **{k: int(r[k]) for k in KEY_FIELDS},
+            "regsPerThread": int(r["regsPerThread"]), "theoretical_waves_per_cu": p["ctasPerSM"] * p["numWarps"],
+            "pred_tflops": round(p["predictedTFLOPS"], 3), "measured_tflops": float(r["tflops"])}
+
+
+def select_configs(sources=SOURCES, hw_json=HW_JSON, per_label=PER_LABEL):
+    """The registered selection rule: every measured row (sweep and BASELINE
+    configs) is labelled by the model; within each label the rows are sorted by
+    (tag, BM, BN, BK, WM, WN, stages, groupM) and the first `per_label` rows of
+    distinct shapes are taken (the reference's rule, ncu-label-mapping.md
+    section 3)."""
+    hw = RM.Hardware(hw_json)
+    groups = {}
+    for src in sources:
+        for r in _read_rows(src):
+            p = predict_row(hw, r)
+            groups.setdefault(p["bottleneck"], []).append((r, p))
+    out = []
+    # The headline bench config, a registered control outside the score: its
+    # one-workgroup-per-CU grid keeps every CU busy for the whole launch, which
+    # checks the counter normalisations (section 2 of the registration).
+    for r in _read_rows(sources[-1]):
+        if tuple(int(r[k]) for k in ["M", "N", "K"] + KEY_FIELDS) == CONTROL:
+            p = predict_row(hw, r)
+            out.append(_config_row("CONTROL", r, p))
+    for label in LABEL_ORDER:
+        rows = sorted(groups.get(label, []),
+                      key=lambda rp: (rp[0]["tag"],) + tuple(int(rp[0][k]) for k in KEY_FIELDS))
+        shapes = set()
+        for r, p in rows:
+            shape = (int(r["M"]), int(r["N"]), int(r["K"]))
+            if shape in shapes:
+                continue
+            shapes.add(shape)
+            out.append(_config_row(label, r, p))
+            if len(shapes) == per_label:
+                break
+    return out
+
+
+CONFIG_COLUMNS = ["predicted_label", "model_label", "tag", "M", "N", "K"] + KEY_FIELDS + \
+    ["regsPerThread", "theoretical_waves_per_cu", "pred_tflops", "measured_tflops"]
+
+
+def cmd_select(args):
+    rows = select_configs()
+    with open(args.out, "w", newline="") as f:
+        f.write("# registered before any rocprofv3 run; see data/sweep/rocprof-label-mapping.md\n")
+        w = csv.DictWriter(f, fieldnames=CONFIG_COLUMNS)
+        w.writeheader()
+        for r in rows:
+            w.writerow(r)
+    for r in rows:
+        print("%-9s %-28s %6dx%-6dx%-5d %dx%dx%d w%dx%d s%d g%d" % (
+            r["predicted_label"], r["tag"], r["M"], r["N"], r["K"], *[r[k] for k in KEY_FIELDS]))
+    print("wrote %d configs to %s" % (len(rows), args.out))
+
+
+def load_configs(path=CONFIGS_CSV):
+    rows = _read_rows(path)
+    for r in rows:
+        for k in ["M", "N", "K"] + KEY_FIELDS + ["regsPerThread", "theoretical_waves_per_cu"]:
+            r[k] = int(r[k])
+    return rows
+
+
+def cmd_run(args):
+    """The launches rocprofv3 observes: per config, LAUNCHES launches of the
+    registered variant, each followed by a synchronize."""
+    import torch
+    from ridge_amd import gemm as G
+    configs = load_configs(args.configs)
+    dev = "cuda:0"
+    cache = {}
+    for i, c in enumerate(configs):
+        idx = G.find_variant(*[c[k] for k in KEY_FIELDS])
+        if idx < 0:
+            raise SystemExit("config %d: variant not in the kernel table" % i)
+        if not G.variant(idx).divides(c["M"], c["N"], c["K"]):
+            raise SystemExit("config %d: variant does not divide the shape" % i)
+        M, N, K = c["M"], c["N"], c["K"]
+        print("config %d/%d %s %dx%dx%d %s" % (i + 1, len(configs), c["predicted_label"], M, N, K,
+                                               G.variant(idx).label()), flush=True)
+        if (M, N, K) not in cache:
+            cache.clear()
+            torch.cuda.synchronize()
+            A = torch.empty((M, K), dtype=torch.float16, device=dev)
+            B = torch.empty((K, N), dtype=torch.float16, device=dev)
+            C = torch.empty((M, N), dtype=torch.float16, device=dev)
+            G.fill_uniform(A, 1)
+            G.fill_uniform(B, 2)
+            cache[(M, N, K)] = (A, B, C)
+        A, B, C = cache[(M, N, K)]
+        torch.cuda.synchronize()
+        for _ in range(args.launches):
+            rc = G.launch(idx, A, B, C, M, N, K)
+            if rc != 0:
+                raise SystemExit("config %d: launch returned %d" % (i, rc))
+            torch.cuda.synchronize()
+    print("labelcheck run: %d configs x %d launches" % (len(configs), args.launches), flush=True)
+
+
+# ---------------------------------------------------------------------------
+# Parsing rocprofv3 CSV output.
+# ---------------------------------------------------------------------------
+
+_GEMM_NAME = re.compile(r"gemmMfma(?:PingPong)?Kernel<\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+)\s*>")
+
+
+def _find(directory, suffix):
+    hits = sorted(glob.glob(os.path.join(directory, "**", "*" + suffix), recursive=True))
+    if not hits:
+        raise SystemExit("no *%s under %s" % (suffix, directory))
+    return hits
+
+
+def parse_counter_dir(directory):
+    """{dispatch_id: {"name": kernel, "counters": {name: [values]}}} for every
+    dispatch of every *counter_collection.csv under `directory`."""
+    out = {}
+    for path in _find(directory, "counter_collection.csv"):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                d = out.setdefault((path, int(r["Dispatch_Id"])), {"name": r["Kernel_Name"], "counters": {}})
+                d["counters"].setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def parse_trace_dir(directory):
+    out = {}
+    for path in _find(directory, "kernel_trace.csv"):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                out[(path, int(r["Dispatch_Id"]))] = {
+                    "name": r["Kernel_Name"], "ns": float(r["End_Timestamp"]) - float(r["Start_Timestamp"])}
+    return out
+
+
+def gemm_dispatches(parsed, configs, launches):
+    """The GEMM dispatches in dispatch order, grouped per config; each name must
+    carry that config's template arguments."""
+    gemm = [(k, v) for k, v in sorted(parsed.items()) if _GEMM_NAME.search(v["name"])]
+    if len(gemm) != len(configs) * launches:
+        raise SystemExit("expected %d GEMM dispatches, found %d" % (len(configs) * launches, len(gemm)))
+    groups = []
+    for i, c in enumerate(configs):
+        chunk = gemm[i * launches:(i + 1) * launches]
+        want = tuple(c[k] for k in KEY_FIELDS)
+        for _, v in chunk:
+            got = tuple(int(x) for x in _GEMM_NAME.search(v["name"]).groups())
+            if got != want:
+                raise SystemExit("config %d: dispatch of %s, expected %s" % (i, got, want))
+        groups.append([v for _, v in chunk])
+    return groups
+
+
+def _counter(dispatch, name, xcds, grbm):
+    vals = dispatch["counters"].get(name)
+    if vals is None:
+        raise SystemExit("counter %s missing from a dispatch" % name)
+    if grbm:
+        # One value per XCD (reported separately or summed): the per-XCD clock
+        # count is the max, or the sum over the XCDs divided by their number.
+        return max(vals) if len(vals) > 1 else vals[0] / xcds
+    return sum(vals)
+
+
+def cmd_gather(args):
+    configs = load_configs(args.configs)
+    with open(HW_JSON) as f:
+        hwj = json.load(f)
+    xcds = int(hwj.get("numXcds", 8))
+    p1 = gemm_dispatches(parse_counter_dir(args.counters), configs, args.launches)
+    pf = gemm_dispatches(parse_counter_dir(args.fetch), configs, args.launches)
+    pw = gemm_dispatches(parse_counter_dir(args.write), configs, args.launches)
+    pt = gemm_dispatches(parse_trace_dir(args.trace), configs, args.launches)
+    rows = []
+    for i, c in enumerate(configs):
+        med = lambda xs: statistics.median(xs)  # noqa: E731
+        row = {k: c[k] for k in CONFIG_COLUMNS}
+        for name in PASS1_COUNTERS:
+            row[name] = med([_counter(d, name, xcds, name.startswith("GRBM_")) for d in p1[i]])
+        row["FETCH_SIZE"] = med([_counter(d, "FETCH_SIZE", xcds, False) for d in pf[i]])
+        row["WRITE_SIZE"] = med([_counter(d, "WRITE_SIZE", xcds, False) for d in pw[i]])
+        row["duration_ns"] = med([d["ns"] for d in pt[i]])
+        rows.append(row)
+    cols = list(rows[0].keys())
+    with open(args.out, "w", newline="") as f:
+        f.write("# rocprofv3 counters per registered config (medians over %d launches); GRBM counters per XCD\n"
+                % args.launches)
+        w = csv.DictWriter(f, fieldnames=cols)
+        w.writeheader()
+        for r in rows:
+            w.writerow(r)
+    print("wrote %d rows to %s" % (len(rows), args.out))
+
+
+# ---------------------------------------------------------------------------
+# Scoring: the registered table and nothing else.
+# ---------------------------------------------------------------------------
+
+def derived(row, hwj):
+    """AMD's derived-counter definitions (rocprofiler-sdk counter_defs.yaml for
+    gfx950: MfmaUtil, LdsUtil, OccupancyPercent, SIMD_UTILIZATION) plus HBM% from
+    the scaled traffic counters over the kernel-trace duration."""
+    cus = float(hwj["numSMs"])
+    simds = cus * float(hwj.get("simdsPerSM", 4))
+    gui = float(row["GRBM_GUI_ACTIVE"])
+    count = float(row["GRBM_COUNT"])
+    out = {}
+    out["mfma_pct"] = 100.0 * float(row["SQ_VALU_MFMA_BUSY_CYCLES"]) / (gui * simds)
+    out["lds_pct"] = 100.0 * float(row["SQ_LDS_IDX_ACTIVE"]) / (gui * cus)
+    out["occ_pct"] = 400.0 * float(row["SQ_WAVE_CYCLES"]) / gui / cus / float(hwj["maxWarpsPerSM"])
+    out["simd_util_pct"] = 100.0 * float(row["SQ_BUSY_CU_CYCLES"]) / count / cus
+    bytes_ = (float(row["FETCH_SIZE"]) * FETCH_SCALE + float(row["WRITE_SIZE"]) * WRITE_SCALE) * 1024.0
+    out["hbm_tbs"] = bytes_ / (float(row["duration_ns"]) * 1e-9) / 1e12
+    out["hbm_pct"] = 100.0 * out["hbm_tbs"] * 1e12 / float(hwj["hbmBytesPerSec"])
+    out["theoretical_occ_pct"] = 100.0 * float(row["theoretical_waves_per_cu"]) / float(hwj["maxWarpsPerSM"])
+    return out
+
+
+def counter_label(d):
+    """The registered decision table (rocprof-label-mapping.md section 2)."""
+    if d["hbm_pct"] >= HBM_PCT_MIN:
+        return "HBM"
+    if d["simd_util_pct"] < SIMD_UTIL_PCT_MAX:
+        return "WAVES"
+    if d["occ_pct"] / d["theoretical_occ_pct"] < OCC_SHORTFALL_MAX:
+        return "OCC"
+    if d["lds_pct"] > d["mfma_pct"]:
+        return "SMEM"
+    if d["mfma_pct"] >= MFMA_PCT_MIN:
+        return "TENSOR_CORE"
+    return "ENVELOPE"
+
+
+def score(rows, hwj):
+    """(results, agree, need, control_ok): results over every row, the count of
+    scored rows (the control excluded) whose counter label equals the model's,
+    the registered pass threshold, and whether the control's SIMD utilisation
+    is in its band (if not, the normalisations are wrong and the run is void)."""
+    results = []
+    control_ok = True
+    for r in rows:
+        d = derived(r, hwj)
+        results.append((r, d, counter_label(d)))
+        if r["predicted_label"] == "CONTROL":
+            lo, hi = CONTROL_SIMD_UTIL_PCT
+            control_ok = control_ok and lo <= d["simd_util_pct"] <= hi
+    scored = [x for x in results if x[0]["predicted_label"] != "CONTROL"]
+    agree = sum(1 for r, d, lab in scored if lab == r["predicted_label"])
+    need = -(-int(PASS_FRACTION * 100) * len(scored) // 100)
+    return results, agree, need, control_ok
+
+
+def cmd_score(args):
+    with open(HW_JSON) as f:
+        hwj = json.load(f)
+    rows = _read_rows(args.counters_csv)
+    results, agree, need, control_ok = score(rows, hwj)
+    print("%-9s %-28s %-22s %6s %6s %6s %6s %6s %6s  %-9s" % (
+        "model", "shape", "variant", "HBM%", "SIMD%", "occ%", "theo%", "LDS%", "MFMA%", "counters"))
+    by_label = {}
+    for r, d, lab in results:
+        shape = "%sx%sx%s" % (r["M"], r["N"], r["K"])
+        var = "%sx%sx%s w%sx%s s%s g%s" % tuple(r[k] for k in KEY_FIELDS)
+        verdict = "" if r["predicted_label"] == "CONTROL" else (
+            "agree" if lab == r["predicted_label"] else "DISAGREE")
+        print("%-9s %-28s %-22s %6.1f %6.1f %6.1f %6.1f %6.1f %6.1f  %-9s %s" % (
+            r["predicted_label"], shape, var, d["hbm_pct"], d["simd_util_pct"], d["occ_pct"],
+            d["theoretical_occ_pct"], d["lds_pct"], d["mfma_pct"], lab, verdict))
+        if r["predicted_label"] == "CONTROL":
+            continue
+        s = by_label.setdefault(r["predicted_label"], [0, 0])
+        s[0] += lab == r["predicted_label"]
+        s[1] += 1
+    print()
+    for lab in LABEL_ORDER:
+        if lab in by_label:
+            print("  %-9s %d of %d agree%s" % (lab, by_label[lab][0], by_label[lab][1],
+                                              "  (fall-through label: weakest evidence)" if lab == "ENVELOPE"
+                                              else ""))
+    if not control_ok:
+        print("\ncontrol SIMD utilisation outside [%g, %g]%%: the normalisations are wrong, the run is VOID"
+              % CONTROL_SIMD_UTIL_PCT)
+        return 2
+    scored = sum(1 for r, d, lab in results if r["predicted_label"] != "CONTROL")
+    verdict = "PASS" if agree >= need else "FAIL"
+    print("\n%d of %d configs agree (registered pass: >= %d) -> %s" % (agree, scored, need, verdict))
+    return 0 if verdict == "PASS" else 1
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("select")
+    s.add_argument("--out", default=CONFIGS_CSV)
+    r = sub.add_parser("run")
+    r.add_argument("--configs", default=CONFIGS_CSV)
+    r.add_argument("--launches", type=int, default=LAUNCHES)
+    g = sub.add_parser("gather")
+    g.add_argument("--configs", default=CONFIGS_CSV)
+    g.add_argument("--launches", type=int, default=LAUNCHES)
+    for k in ("counters", "fetch", "write", "trace"):
+        g.add_argument("--" + k, required=True)
+    g.add_argument("--out", default=COUNTERS_CSV)
+    c = sub.add_parser("score")
+    c.add_argument("--counters-csv", default=COUNTERS_CSV)
+    args = ap.parse_args(argv)
+    return {"select": cmd_select, "run": cmd_run, "gather": cmd_gather, "score": cmd_score}[args.cmd](args)
+
+
+if __name__ == "__main__":
+    sys.exit(main() or 0)

@@ -229,7 +229,7 @@ def main(argv=None):
     labels = collections.Counter(r["pred_bottleneck"] for r in rows)
     print("bottleneck attribution")
     print("  predicted label distribution: %s" % dict(labels))
-    print("  cross-checked against rocprofv3 counters: see profiles/ (label mapping is registered there)")
+    print("  counter cross-check: python -m ridge_amd.labelcheck (registered in data/sweep/rocprof-label-mapping.md)")
     print()
     print("=" * 74)
     print("MAPE %.2f%%, mean Spearman %.3f, worst regret@1 %.2f%%" % (

@@ -1,0 +1,118 @@
+"""The rocprofv3 label check's registration, selection, parsing and decision
+table, on the CPU (the counters themselves come from the GPU box)."""
+import csv
+import os
+import re
+
+import pytest
+
+from ridge_amd import labelcheck as LC
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REG = os.path.join(ROOT, "data", "sweep", "rocprof-label-mapping.md")
+
+
+def test_committed_config_list_is_the_registered_selection(tmp_path):
+    out = tmp_path / "c.csv"
+    LC.main(["select", "--out", str(out)])
+    with open(out) as a, open(LC.CONFIGS_CSV) as b:
+        assert a.read() == b.read()
+
+
+def test_selection_rule_distinct_shapes_per_label():
+    rows = LC.load_configs()
+    assert rows[0]["predicted_label"] == "CONTROL"
+    scored = rows[1:]
+    labels = [r["predicted_label"] for r in scored]
+    for lab in set(labels):
+        shapes = [(r["M"], r["N"], r["K"]) for r in scored if r["predicted_label"] == lab]
+        assert len(shapes) == len(set(shapes)) <= LC.PER_LABEL
+        assert all(r["model_label"] == lab for r in scored if r["predicted_label"] == lab)
+    # Groups appear in the registered order, each sorted by tag then tile.
+    order = [LC.LABEL_ORDER.index(x) for x in labels]
+    assert order == sorted(order)
+
+
+def _d(**kw):
+    base = dict(hbm_pct=10.0, simd_util_pct=99.0, occ_pct=25.0, theoretical_occ_pct=25.0, lds_pct=20.0,
+                mfma_pct=50.0)
+    base.update(kw)
+    return base
+
+
+def test_decision_table_first_match_wins():
+    assert LC.counter_label(_d()) == "ENVELOPE"
+    assert LC.counter_label(_d(hbm_pct=70.0, simd_util_pct=10.0)) == "HBM"
+    assert LC.counter_label(_d(hbm_pct=69.9, simd_util_pct=79.9)) == "WAVES"
+    assert LC.counter_label(_d(occ_pct=17.4, theoretical_occ_pct=25.0)) == "OCC"     # 0.696
+    assert LC.counter_label(_d(occ_pct=17.6, theoretical_occ_pct=25.0)) == "ENVELOPE"  # 0.704
+    assert LC.counter_label(_d(lds_pct=50.1, mfma_pct=50.0)) == "SMEM"
+    assert LC.counter_label(_d(lds_pct=50.0, mfma_pct=50.0)) == "ENVELOPE"            # not strictly greater
+    assert LC.counter_label(_d(mfma_pct=70.0)) == "TENSOR_CORE"
+    # WAVES is decided before SMEM: an idle machine with a busy LDS is WAVES.
+    assert LC.counter_label(_d(simd_util_pct=50.0, lds_pct=90.0)) == "WAVES"
+
+
+def test_registration_text_matches_the_code():
+    text = open(REG).read()
+    assert re.search(r"\| 1 \| HBM% ≥ (\d+) \| `HBM` \|", text).group(1) == "%g" % LC.HBM_PCT_MIN
+    assert re.search(r"\| 2 \| SIMD% < (\d+) \| `WAVES` \|", text).group(1) == "%g" % LC.SIMD_UTIL_PCT_MAX
+    assert float(re.search(r"\| 3 \| occ% / theoretical occ% < ([0-9.]+) \| `OCC` \|", text).group(1)) == \
+        LC.OCC_SHORTFALL_MAX
+    assert "| 4 | LDS% > MFMA% | `SMEM` |" in text
+    assert re.search(r"\| 5 \| MFMA% ≥ (\d+) \| `TENSOR_CORE` \|", text).group(1) == "%g" % LC.MFMA_PCT_MIN
+    assert "At least %d%% of the" % int(LC.PASS_FRACTION * 100) in text
+    n = len(LC.load_configs()) - 1
+    assert "%d scored configs (%d of %d)" % (n, -(-75 * n // 100), n) in text
+
+
+def test_derived_quantities_use_amd_definitions():
+    hwj = {"numSMs": 256, "simdsPerSM": 4, "maxWarpsPerSM": 32, "hbmBytesPerSec": 5e12}
+    row = {"GRBM_GUI_ACTIVE": 1000.0, "GRBM_COUNT": 1000.0, "SQ_VALU_MFMA_BUSY_CYCLES": 512000.0,
+           "SQ_LDS_IDX_ACTIVE": 64000.0, "SQ_WAVE_CYCLES": 512000.0, "SQ_BUSY_CU_CYCLES": 256000.0,
+           "FETCH_SIZE": 1000.0, "WRITE_SIZE": 500.0, "duration_ns": 1000.0, "theoretical_waves_per_cu": 8}
+    d = LC.derived(row, hwj)
+    assert d["mfma_pct"] == pytest.approx(50.0)      # 512000 / (1000 * 1024)
+    assert d["lds_pct"] == pytest.approx(25.0)       # 64000 / (1000 * 256)
+    # 8 waves per CU for 1000 cycles = 2000 wave-quad-cycles per CU, x 256 CUs:
+    # 400 * 512000 / 1000 / 256 / 32 = 25% of the 32 wave slots
+    assert d["occ_pct"] == pytest.approx(25.0)
+    assert d["simd_util_pct"] == pytest.approx(100.0)
+    assert d["theoretical_occ_pct"] == pytest.approx(25.0)
+    # (1000 * 2 + 500) KiB in 1 us = 2.56 GB/ms = 2.56 TB/s
+    assert d["hbm_tbs"] == pytest.approx(2500 * 1024 / 1e-6 / 1e12)
+
+
+def _write_counter_csv(path, dispatches):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        for did, name, counters in dispatches:
+            for cn, vals in counters.items():
+                for v in vals:
+                    w.writerow([did, name, cn, v])
+
+
+def test_gather_groups_dispatches_by_order_and_checks_names(tmp_path):
+    configs = [dict(M=256, N=256, K=64, BM=64, BN=64, BK=32, WM=32, WN=32, stages=4, groupM=8),
+               dict(M=512, N=512, K=64, BM=128, BN=128, BK=32, WM=64, WN=64, stages=4, groupM=8)]
+    names = ["void ridge::gemmMfmaKernel<64, 64, 32, 32, 32, 4, 8>(_Float16 const*)",
+             "void ridge::gemmMfmaKernel<128, 128, 32, 64, 64, 4, 8>(_Float16 const*)"]
+    disp = [(1, "fillUniformKernel", {"GRBM_GUI_ACTIVE": [5.0]})]
+    did = 2
+    for c, n in zip(configs, names):
+        for j in range(2):
+            disp.append((did, n, {"GRBM_GUI_ACTIVE": [100.0 * did] * 8}))
+            did += 1
+    d = tmp_path / "p" / "host" / "123"
+    d.mkdir(parents=True)
+    _write_counter_csv(d / "run_counter_collection.csv", disp)
+    groups = LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), configs, 2)
+    assert [len(g) for g in groups] == [2, 2]
+    # eight per-XCD rows: the max is the per-XCD count
+    assert LC._counter(groups[1][0], "GRBM_GUI_ACTIVE", 8, True) == 400.0
+    bad = [dict(configs[0]), dict(configs[1], groupM=4)]
+    with pytest.raises(SystemExit, match="expected"):
+        LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), bad, 2)
+    with pytest.raises(SystemExit, match="expected 6 GEMM dispatches"):
+        LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), configs, 3)
