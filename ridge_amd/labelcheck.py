@@ -184,7 +184,16 @@ def cmd_run(args):
 # Parsing rocprofv3 CSV output.
 # ---------------------------------------------------------------------------
 
-_GEMM_NAME = re.compile(r"gemmMfma(?:PingPong)?Kernel<\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+),\s*(\d+)\s*>")
+# Kernel names as rocprofv3 reports them: Itanium-mangled, each int template
+# argument as Li<n>E (gemmMfmaKernelILi64ELi64E...), or demangled (<64, 64, ...>).
+_GEMM_NAME = re.compile(r"gemmMfma(?:PingPong)?Kernel(?:I" + r"Li(\d+)E" * 7 + r"|<" +
+                        r",".join([r"\s*(\d+)"] * 7) + r"\s*>)")
+
+
+def _template_args(name):
+    m = _GEMM_NAME.search(name)
+    vals = [g for g in m.groups() if g is not None]
+    return tuple(int(x) for x in vals)
 
 
 def _find(directory, suffix):
@@ -227,7 +236,7 @@ def gemm_dispatches(parsed, configs, launches):
         chunk = gemm[i * launches:(i + 1) * launches]
         want = tuple(c[k] for k in KEY_FIELDS)
         for _, v in chunk:
-            got = tuple(int(x) for x in _GEMM_NAME.search(v["name"]).groups())
+            got = _template_args(v["name"])
             if got != want:
                 raise SystemExit("config %d: dispatch of %s, expected %s" % (i, got, want))
         groups.append([v for _, v in chunk])
