@@ -8,6 +8,15 @@
 // swept (one workgroup per CU) because "CU-level" only means something once all
 // four SIMDs are busy: one wave drives one SIMD, four waves saturate the CU.
 //
+// The matrix instructions are issued through inline asm with the accumulator
+// tied to the destination (dst == srcC), so the timed stream is nothing but
+// MFMAs: issued as builtins, the compiler renames accumulators here and inserts
+// register copies between the MFMAs, which cost one wave a third of its issue
+// rate (24 cycles per instruction per SIMD against 16.9 for the clean stream)
+// and made the low-wave columns of the curve measure the copies. Independent
+// chains are kIlp MFMAs apart, far beyond the result latency, so no wait states
+// are needed between them.
+//
 // Operands are the GEMM's: random U[-1,1) halves, a different fragment pair on
 // every instruction (eight of each, rotated). MI355X is power-limited under a
 // full-chip matrix load, and the loaded clock depends on how many operand bits
@@ -68,8 +77,9 @@ __global__ __launch_bounds__(Waves * 64) void mfmaThroughputKernel(const half8_t
             for (int u = 0; u < kInner; ++u)
 #pragma unroll
                 for (int j = 0; j < kIlp; ++j)
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[(j + u) % kFrags], b[(3 * j + u) % kFrags],
-                                                                    acc[j], 0, 0, 0);
+                    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                                 : "+v"(acc[j])
+                                 : "v"(a[(j + u) % kFrags]), "v"(b[(3 * j + u) % kFrags]));
         }
         __syncthreads();
         c1 = cycles();
@@ -91,8 +101,9 @@ __global__ __launch_bounds__(Waves * 64) void mfmaThroughputKernel(const half8_t
             for (int u = 0; u < kInner; ++u)
 #pragma unroll
                 for (int j = 0; j < kIlp / 2; ++j)
-                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[(j + u) % kFrags], b[(3 * j + u) % kFrags],
-                                                                    acc[j], 0, 0, 0);
+                    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0"
+                                 : "+v"(acc[j])
+                                 : "v"(a[(j + u) % kFrags]), "v"(b[(3 * j + u) % kFrags]));
         }
         __syncthreads();
         c1 = cycles();

@@ -33,7 +33,10 @@ import sys
 from ridge_amd import model as RM
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HW_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+# The calibration the registration was made under (a frozen copy of
+# data/hardware/mi355x.json at registration time): selection and scoring use it,
+# so a later re-calibration cannot change the registered configs or thresholds.
+HW_JSON = os.path.join(ROOT, "data", "sweep", "rocprof-label-hw.json")
 SOURCES = [os.path.join(ROOT, "data", "measured", "mi355x.csv"),
            os.path.join(ROOT, "data", "measured", "mi355x-baseline-configs.csv")]
 CONFIGS_CSV = os.path.join(ROOT, "data", "sweep", "rocprof-label-configs.csv")
