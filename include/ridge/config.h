@@ -36,6 +36,11 @@ struct GemmConfig {
     // Registers per lane of the real kernel (VGPR + AGPR on CDNA, ptxas count on
     // sm_80). 0 = unknown: register occupancy is not applied.
     int regsPerThread = 128;
+
+    // Launch-order group size along M (the kernel's GroupM). Only the exact
+    // launch-order reuse model (HardwareModel::l2ReuseModel 2) reads it; the
+    // reference model has no such field.
+    int groupM = 8;
 };
 
 }  // namespace ridge

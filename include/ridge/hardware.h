@@ -46,6 +46,8 @@ struct HardwareModel {
     int cBytes = 4;                  // bytes per output element drained by the epilogue
     int l2ReuseModel = 0;            // 0: sqrt(ctaSlots) square reuse (reference)
                                      // 1: per-XCD resident block, bounded by the grid
+                                     // 2: the kernels' exact launch order (XCD remap of
+                                     //    the GroupM order): distinct panels per XCD
     int prologueModel = 0;           // 0: the prologue always fills stages-1 tiles (reference)
                                      // 1: only the K tiles that exist, min(stages-1, K/BK)
     int pingPongModel = 0;           // 0: operand reads in series with the MFMAs (reference)

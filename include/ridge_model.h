@@ -26,6 +26,7 @@ typedef struct ridge_model_config {
     int mmaM, mmaN, mmaK;   /* 0 = the hardware model's instruction shape */
     int stages;
     int regsPerThread;      /* 0 = unknown */
+    int groupM;             /* launch-order group size along M (read by l2ReuseModel 2 only) */
 } ridge_model_config_t;
 
 typedef struct ridge_model_prediction {

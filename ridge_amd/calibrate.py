@@ -121,7 +121,7 @@ def hardware_json(res, spec, arch):
         "regGranule": 8,
         "numXcds": 8,
         "cBytes": 2,
-        "l2ReuseModel": 1,
+        "l2ReuseModel": 2,
         "prologueModel": 1,
         "pingPongModel": 1,
         "warpsNeededToHideIlp8": res.get("warpsNeededToHideIlp8", 0.0),

@@ -63,7 +63,7 @@ HardwareModel HardwareModel::mi355x() {
     h.regGranule = 8;
     h.numXcds = 8;
     h.cBytes = 2;
-    h.l2ReuseModel = 1;
+    h.l2ReuseModel = 2;
     h.prologueModel = 1;
     h.pingPongModel = 1;
     return h;

@@ -17,6 +17,9 @@
 //                           the grid, and fetch their A and B panels once into
 //                           that XCD's L2; capped by the compulsory intensity of
 //                           the whole problem                 (reference :116-123)
+//                         = hw.l2ReuseModel 2: the same from the kernels' exact
+//                           launch order (XCD remap of the GroupM order), so
+//                           groupM changes the prediction
 //   K-step time           = hw.pingPongModel 1: max(compute, operand reads) for a
 //                           workgroup of two waves per SIMD with >= 3 stages (the
 //                           ping-pong schedule), their sum otherwise (reference :47)
@@ -35,6 +38,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <vector>
 
 namespace ridge {
 
@@ -193,6 +197,54 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         const double l2ReuseFactor = std::sqrt(ctaSlots);
         arithmeticIntensity = baseIntensity * l2ReuseFactor;
         p.l2ReuseFactor = l2ReuseFactor;
+    } else if (hw.l2ReuseModel == 2) {
+        // The kernels' launch order, exactly. Hardware workgroup p runs on XCD
+        // p % X; the kernel maps it to logical id xcdRemap(p) = x*q + min(x, r) +
+        // p / X (q, r = totalCtas / X, % X), and the logical id to a tile by the
+        // GroupM order. The first n = min(slots, tiles) workgroups are resident
+        // together; XCD x holds the first ceil((n - x) / X) ids of its range. Each
+        // XCD fetches every distinct A row panel and B column panel of its
+        // resident tiles once into its own L2; the traffic is summed over XCDs.
+        const long long numPidM = cfg.M / cfg.BM;
+        const long long numPidN = cfg.N / cfg.BN;
+        const long long total = numPidM * numPidN;
+        const long long n = (long long)std::min(ctaSlots, totalCtas);
+        const long long X = hw.numXcds;
+        const long long q = total / X, r = total % X;
+        const long long G = std::max(1, cfg.groupM);
+        std::vector<long long> rowSeen(numPidM, -1), colSeen(numPidN, -1);
+        double rowPanels = 0.0, colPanels = 0.0;
+        for (long long x = 0; x < X && x < n; ++x) {
+            const long long base = x * q + std::min(x, r);
+            const long long count = (n - x + X - 1) / X;
+            for (long long j = 0; j < count; ++j) {
+                const long long pid = base + j;
+                const long long pidInGroup = pid % (G * numPidN);
+                const long long firstPidM = (pid / (G * numPidN)) * G;
+                const long long groupRows = std::min(numPidM - firstPidM, G);
+                const long long row = firstPidM + pidInGroup % groupRows;
+                const long long col = pidInGroup / groupRows;
+                if (rowSeen[row] != x) {
+                    rowSeen[row] = x;
+                    rowPanels += 1.0;
+                }
+                if (colSeen[col] != x) {
+                    colSeen[col] = x;
+                    colPanels += 1.0;
+                }
+            }
+        }
+        const double residentFlops = 2.0 * double(n) * cfg.BM * cfg.BN * double(cfg.K);
+        const double residentBytes = (rowPanels * cfg.BM + colPanels * cfg.BN) * double(cfg.K) * db;
+        const double l2Intensity = residentFlops / residentBytes;
+        const double M = double(cfg.M), N = double(cfg.N), K = double(cfg.K);
+        const double compulsory = 2.0 * M * N * K / ((M * K + K * N) * db + M * N * hw.cBytes);
+        arithmeticIntensity = std::min(l2Intensity, compulsory);
+        p.l2ReuseFactor = arithmeticIntensity / baseIntensity;
+        const double xcdsUsed = double(std::min(X, n));
+        p.reuseTilesM = rowPanels / xcdsUsed;
+        p.reuseTilesN = colPanels / xcdsUsed;
+        p.compulsoryIntensity = compulsory;
     } else {
         // The workgroups resident on one XCD at a time, as compact a block of
         // output tiles as the grid allows: a rows x b columns of tiles. Each XCD

@@ -34,6 +34,7 @@ GemmConfig toCpp(const ridge_model_config_t& c) {
     g.mmaK = c.mmaK;
     g.stages = c.stages;
     g.regsPerThread = c.regsPerThread;
+    g.groupM = c.groupM;
     return g;
 }
 
@@ -57,6 +58,7 @@ void ridge_model_default_config(ridge_model_config_t* cfg) {
     cfg->mmaK = g.mmaK;
     cfg->stages = g.stages;
     cfg->regsPerThread = g.regsPerThread;
+    cfg->groupM = g.groupM;
 }
 
 void* ridge_model_hw_load(const char* spec, char* err, size_t errcap) {

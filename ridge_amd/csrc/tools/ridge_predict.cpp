@@ -95,6 +95,7 @@ int runBatch(const std::string& inPath, const std::string& outPath, const Hardwa
         cfg.warpN = int(col("WN", cfg.warpN));
         cfg.stages = int(col("stages", cfg.stages));
         cfg.regsPerThread = int(col("regsPerThread", cfg.regsPerThread));
+        cfg.groupM = int(col("groupM", cfg.groupM));
         const Prediction p = predict(cfg, hw);
         out << line << ',' << p.predictedTFLOPS << ',' << toString(p.bottleneck) << ',' << p.computeTFLOPS << ','
             << p.hbmTFLOPS << ',' << p.smEfficiency << ',' << p.occFactor << ',' << p.arithmeticIntensity << ','

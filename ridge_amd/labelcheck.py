@@ -76,7 +76,7 @@ def _read_rows(path):
 def predict_row(hw, r):
     return RM.predict(hw, M=int(r["M"]), N=int(r["N"]), K=int(r["K"]), BM=int(r["BM"]), BN=int(r["BN"]),
                       BK=int(r["BK"]), warpM=int(r["WM"]), warpN=int(r["WN"]), stages=int(r["stages"]),
-                      regsPerThread=int(r["regsPerThread"]))
+                      regsPerThread=int(r["regsPerThread"]), groupM=int(r["groupM"]))
 
 
 def _config_row(label, r, p):

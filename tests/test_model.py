@@ -130,10 +130,13 @@ def test_mi355x_worked_example(mi355x):
       peak           16384 / 4 x 2.4e9 x 256 = 2516.5824 TFLOP/s
       compute        2516.5824 x 0.571429 x 0.938237 = 1349.22
       base AI        2 x 256 x 256 x 4096 / ((256 + 256) x 4096 x 2) = 128
-      per-XCD block  32 slots per XCD: a = floor(sqrt 32) = 5, b = ceil(32/5) = 7,
-                     a = ceil(32/7) = 5; AI = (5x256)(7x256)/((5+7)x256) = 746.667
-      compulsory     2 x 4096^3 / (3 x 4096^2 x 2) = 1365.33; AI = 746.667
-      HBM            8e12 x 746.667 = 5973.33 TFLOP/s; label SMEM (0.571 worst)
+      launch order   256 tiles, all resident, 32 per XCD: XCD 0 runs logical ids
+                     0..31; groupM 8 (the config default): group = 8 rows x 16
+                     columns, ids 0..31 -> rows 0..7 (id % 8), columns 0..3 (id / 8)
+                     -> 8 A panels + 4 B panels; AI = 2 x 32 x 256^2 x 4096 /
+                     ((8 + 4) x 256 x 4096 x 2) = 682.667
+      compulsory     2 x 4096^3 / (3 x 4096^2 x 2) = 1365.33; AI = 682.667
+      HBM            8e12 x 682.667 = 5461.33 TFLOP/s; label SMEM (0.571 worst)
     """
     p = RM.predict(mi355x, M=4096, N=4096, K=4096, BM=256, BN=256, BK=64, warpM=128, warpN=64, stages=2,
                    regsPerThread=214)
@@ -149,11 +152,27 @@ def test_mi355x_worked_example(mi355x):
     assert p["peakTensorTFLOPS"] == pytest.approx(2516.5824, abs=1e-6)
     assert p["computeTFLOPS"] == pytest.approx(2516.5824 * (2048 / 3584) * (229376 / 244475.4944), abs=1e-6)
     assert p["baseIntensity"] == pytest.approx(128.0)
+    assert (p["reuseTilesM"], p["reuseTilesN"]) == (8.0, 4.0)
+    assert p["arithmeticIntensity"] == pytest.approx(2048 / 3, abs=1e-9)
+    assert p["compulsoryIntensity"] == pytest.approx(2 * 4096 / 6, abs=1e-9)
+    assert p["hbmTFLOPS"] == pytest.approx(8 * 2048 / 3, abs=1e-6)
+    assert p["bottleneck"] == "SMEM"
+
+
+def test_compact_block_reuse_model(tmp_path):
+    """l2ReuseModel 1 (the grid-bounded compact block, no launch order) on the
+    worked example's config: 32 slots per XCD, a = floor(sqrt 32) = 5, b =
+    ceil(32/5) = 7, a = ceil(32/7) = 5; AI = (5x256)(7x256)/((5+7)x256) = 746.667."""
+    cfg = ('{"name": "x", "arch": "gfx950", "numSMs": 256, "clockHz": 2.4e9, "mmaCyclesPerInst": 4, '
+           '"smemBytesPerCycle": 128, "hbmBytesPerSec": 8e12, "regsPerSM": 131072, "smemBytesPerSM": 163840, '
+           '"maxWarpsPerSM": 32, "maxCtasPerSM": 32, "warpsNeededToHide": 8, "l2ReuseModel": 1}')
+    f = tmp_path / "m1.json"
+    f.write_text(cfg)
+    p = RM.predict(RM.Hardware(str(f)), M=4096, N=4096, K=4096, BM=256, BN=256, BK=64, warpM=128, warpN=64,
+                   stages=2, regsPerThread=214)
     assert (p["reuseTilesM"], p["reuseTilesN"]) == (5.0, 7.0)
     assert p["arithmeticIntensity"] == pytest.approx(1280 * 1792 / 3072, abs=1e-9)
-    assert p["compulsoryIntensity"] == pytest.approx(2 * 4096 / 6, abs=1e-9)
     assert p["hbmTFLOPS"] == pytest.approx(8 * 1280 * 1792 / 3072, abs=1e-6)
-    assert p["bottleneck"] == "SMEM"
 
 
 def test_mi355x_ping_pong_overlap_and_prologue_of_existing_tiles(mi355x):
@@ -219,6 +238,29 @@ def test_mi355x_latency_hiding_uses_the_ilp8_column(tmp_path):
     small = dict(BM=64, BN=64, BK=32, warpM=32, warpN=32, stages=4, regsPerThread=62)
     p = RM.predict(RM.Hardware(str(with_ilp)), **small)
     assert p["ctasPerSM"] == 5 and p["occFactor"] == pytest.approx(1.0)
+
+
+def test_mi355x_launch_order_reuse_follows_groupm(mi355x):
+    """8192 x 8192 x 1024, 256x256 tiles (32 x 32 = 1024 tiles), one workgroup per
+    CU: 256 resident, 32 per XCD. XCD x runs logical ids x*128 .. x*128 + 31
+    (xcdRemap: q = 1024 / 8 = 128). groupM = 1 (row-major): ids 0..31 are one row
+    of tiles -> 1 A row panel + 32 B column panels per XCD; intensity
+    2*32*256^2*1024 / ((1*256 + 32*256) * 1024 * 2) = 248.24 FLOP/B. groupM = 4:
+    pidInGroup 0..31 -> rows 0..3, columns 0..7 -> 4 + 8 panels -> 682.67.
+    groupM = 16: 16 rows x 2 columns -> 455.11. The HBM ceiling is the
+    placeholder's 8e12 B/s times the intensity."""
+    cfg = dict(M=8192, N=8192, K=1024, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=4, regsPerThread=197)
+    want = {1: (1, 32, 2 * 32 * 256 * 256 / (33 * 256 * 2)), 4: (4, 8, 2 * 32 * 256 * 256 / (12 * 256 * 2)),
+            16: (16, 2, 2 * 32 * 256 * 256 / (18 * 256 * 2))}
+    for g, (rows, cols, ai) in want.items():
+        p = RM.predict(mi355x, groupM=g, **cfg)
+        assert (p["reuseTilesM"], p["reuseTilesN"]) == (rows, cols), g
+        assert p["arithmeticIntensity"] == pytest.approx(ai, rel=1e-12), g
+        assert p["hbmTFLOPS"] == pytest.approx(8e12 * ai / 1e12, rel=1e-12), g
+    assert want[1][2] == pytest.approx(248.2424, abs=1e-4)
+    # The A100 (reference) model ignores groupM.
+    a100 = RM.Hardware("a100")
+    assert RM.predict(a100, groupM=1, **cfg)["predictedTFLOPS"] == RM.predict(a100, groupM=8, **cfg)["predictedTFLOPS"]
 
 
 def test_mi355x_register_occupancy_per_simd(mi355x):
