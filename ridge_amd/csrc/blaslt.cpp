@@ -88,10 +88,11 @@ int ridge_blaslt_destroy(void* handle) {
     Handle* h = static_cast<Handle*>(handle);
     if (h == nullptr) return 0;
     for (auto& kv : h->plans) destroyPlan(kv.second);
-    if (h->workspace) hipFree(h->workspace);
+    hipError_t err = hipSuccess;
+    if (h->workspace) err = hipFree(h->workspace);
     if (h->lt) hipblasLtDestroy(h->lt);
     delete h;
-    return 0;
+    return (int)err;
 }
 
 int ridge_blaslt_prepare(void* handle, const void* A, const void* B, void* C, int M, int N, int K, int c_is_f32,
@@ -127,10 +128,10 @@ int ridge_blaslt_prepare(void* handle, const void* A, const void* B, void* C, in
     }
     int best = -1;
     float bestMs = 1e30f;
-    hipEvent_t e0, e1;
-    hipEventCreate(&e0);
-    hipEventCreate(&e1);
-    for (int c = 0; c < returned; ++c) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t err = hipEventCreate(&e0);
+    if (err == hipSuccess) err = hipEventCreate(&e1);
+    for (int c = 0; c < returned && err == hipSuccess; ++c) {
         if (res[c].state != HIPBLAS_STATUS_SUCCESS || res[c].workspaceSize > kWorkspaceBytes) continue;
         p.algo = res[c].algo;
         p.workspace = res[c].workspaceSize;
@@ -139,19 +140,24 @@ int ridge_blaslt_prepare(void* handle, const void* A, const void* B, void* C, in
             best = c;
             break;
         }
-        hipEventRecord(e0, s);
-        for (int i = 0; i < iters; ++i) run(h, p, A, B, C, s);
-        hipEventRecord(e1, s);
-        hipEventSynchronize(e1);
+        err = hipEventRecord(e0, s);
+        for (int i = 0; i < iters && err == hipSuccess; ++i)
+            if (run(h, p, A, B, C, s) != 0) err = hipErrorLaunchFailure;
+        if (err == hipSuccess) err = hipEventRecord(e1, s);
+        if (err == hipSuccess) err = hipEventSynchronize(e1);
         float ms = 0.0f;
-        hipEventElapsedTime(&ms, e0, e1);
-        if (ms < bestMs) {
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+        if (err == hipSuccess && ms < bestMs) {
             bestMs = ms;
             best = c;
         }
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    if (e0) (void)hipEventDestroy(e0);  // teardown: nothing to recover from
+    if (e1) (void)hipEventDestroy(e1);
+    if (err != hipSuccess) {
+        destroyPlan(p);
+        return (int)err;
+    }
     if (best < 0) {
         destroyPlan(p);
         return (int)HIPBLAS_STATUS_NOT_SUPPORTED;

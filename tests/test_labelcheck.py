@@ -117,3 +117,21 @@ def test_gather_groups_dispatches_by_order_and_checks_names(tmp_path):
         LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), bad, 2)
     with pytest.raises(SystemExit, match="expected 6 GEMM dispatches"):
         LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), configs, 3)
+
+
+def test_committed_counters_score_as_reported():
+    """The committed counters through the registered table give the reported
+    result (5 of 13, FAIL; control in band) and the per-label split."""
+    import json
+    with open(LC.HW_JSON) as f:
+        hwj = json.load(f)
+    rows = LC._read_rows(LC.COUNTERS_CSV)
+    results, agree, need, control_ok = LC.score(rows, hwj)
+    assert control_ok and (agree, need) == (5, 10)
+    split = {}
+    for r, d, lab in results:
+        if r["predicted_label"] != "CONTROL":
+            s = split.setdefault(r["predicted_label"], [0, 0])
+            s[0] += lab == r["predicted_label"]
+            s[1] += 1
+    assert split == {"SMEM": [0, 4], "WAVES": [4, 4], "ENVELOPE": [0, 4], "HBM": [1, 1]}
