@@ -159,3 +159,41 @@ def test_hipblaslt_comparator_agrees_with_oracle():
     assert O.passes(O.f16_bits_to_f32(_bits(C16)), ref, 0.5, 0.5, K)[0]
     assert O.passes(C32.cpu().numpy(), ref, 0.5, 0.5, K)[0]
     blas.close()
+
+
+def _registered_sweep_shapes():
+    import os
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "data", "sweep",
+                        "mi355x-registered.csv")
+    shapes = []
+    with open(path) as f:
+        for line in f:
+            if line.startswith("#") or not line.strip():
+                continue
+            m, n, k = (int(x) for x in line.split(",")[:3])
+            shapes.append((m, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize("M,N,K", _registered_sweep_shapes())
+def test_registered_sweep_shapes_every_variant(M, N, K):
+    """Every registered sweep shape x every variant (the measured cross product):
+    no output left unwritten (C starts as NaN) and 16 rows spread over M, first and
+    last included, within the reference's tolerances of the f64 oracle."""
+    print("sweep shape %dx%dx%d" % (M, N, K), flush=True)
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, 11)
+    G.fill_uniform(B, 12)
+    rows = np.linspace(0, M - 1, 16).astype(int)
+    Ab = A[torch.from_numpy(rows).to(DEV)].cpu().view(torch.int16).numpy().view(np.uint16).ravel()
+    ref = O.gemm_f64(Ab, _bits(B), len(rows), N, K)
+    idx = torch.from_numpy(rows).to(DEV)
+    for v in G.variants():
+        assert v.divides(M, N, K), v.label()
+        C = _run(v.index, A, B, M, N, K)
+        assert not bool(torch.isnan(C).any()), "%s left outputs unwritten at %dx%dx%d" % (v.label(), M, N, K)
+        got = O.f16_bits_to_f32(C[idx].cpu().view(torch.int16).numpy().view(np.uint16)).reshape(len(rows), N)
+        ok, frob, mx, ne = O.passes(got, ref, 1.0, 1.0, K)
+        assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
+        del C
