@@ -2,7 +2,8 @@
 """Headline benchmark: FP16 GEMM TFLOP/s at 4096^3 on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant BM,BN,BK,WM,WN,S,G]
-                    [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt]
+                    [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt] [--no-cold]
+                    [--allow-partitioned]
     python bench.py --mode copy     # plain device copy of known size, for scaling
                                     # rocprofv3 FETCH_SIZE / WRITE_SIZE counters
 
@@ -14,6 +15,12 @@ bracketed by HIP events on the launch stream for the roofline figure, and the
 hipBLASLt comparator (best of its heuristic candidates, best of a before and an
 after reading, as the reference does in bench/check-gemm.cu:357-391) is timed the
 same way. Prints ONE JSON line.
+
+cold: the same launches (ours and hipBLASLt's) rotated over enough operand sets
+that twice the 256 MB MALL is touched between two uses of one set, so every
+launch reads A and B from HBM; `value` is the warm figure (one operand set,
+re-used, as the reference times). A device that is not a whole MI355X (gfx950,
+256 CUs; a CPX/DPX partition is smaller) is refused unless --allow-partitioned.
 
 cpu_baseline: the CPU f64 GEMM of the oracle (a port of the reference's CPU
 reference, bench/check-gemm.cu:98-108, row-parallel with OpenMP) timed on a
@@ -40,8 +47,9 @@ sys.path.insert(0, ROOT)
 PEAK_FP16_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0
 DEFAULT_SHAPE = (4096, 4096, 4096)
-# The registered variant the sweep measured fastest at 4096^3.
-DEFAULT_VARIANT = (256, 256, 32, 128, 64, 4, 4)
+# The registered variant measured fastest at 4096^3 (the BASELINE-config
+# measurement, data/measured/mi355x-baseline-configs.csv).
+DEFAULT_VARIANT = (256, 256, 32, 128, 64, 3, 4)
 PROFILES = os.path.join(ROOT, "profiles")
 MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x.csv")
 HARDWARE_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
@@ -89,6 +97,54 @@ def roofline(M, N, K, per_launch_ms, traffic):
     achieved = nbytes / sec / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic}
+
+
+# Infinity Cache (MALL) of MI355X: 256 MB, shared by all XCDs in front of HBM.
+MALL_BYTES = 256 << 20
+WHOLE_DEVICE_CUS = 256
+
+
+def device_check(allow_partitioned):
+    """Refuse anything but a whole MI355X (gfx950, 256 CUs): a compute-partitioned
+    GPU (CPX, DPX) shows a fraction of the CUs and XCDs as its own device, which
+    the sweep and the calibration do not describe (the reference refuses a MIG
+    slice the same way, setup-box.sh:37-41). Returns the device description."""
+    import torch
+    p = torch.cuda.get_device_properties(0)
+    arch = getattr(p, "gcnArchName", "")
+    info = {"name": p.name, "arch": arch, "cus": p.multi_processor_count}
+    if not (arch.startswith("gfx950") and p.multi_processor_count == WHOLE_DEVICE_CUS):
+        msg = "device %s (%s, %d CUs) is not a whole MI355X (gfx950, %d CUs)" % (
+            p.name, arch, p.multi_processor_count, WHOLE_DEVICE_CUS)
+        if not allow_partitioned:
+            raise SystemExit(msg + "; pass --allow-partitioned to run anyway")
+        print(msg + "; continuing (--allow-partitioned)", file=sys.stderr)
+    return info
+
+
+def cold_sets(set_bytes):
+    """Number of operand sets to rotate through so that at least twice the MALL's
+    capacity of other sets is touched between two uses of one set."""
+    return max(3, 1 + -(-2 * MALL_BYTES // set_bytes))
+
+
+def time_cold(make_step, sets, steps, stream):
+    """HIP-event milliseconds per launch with launch i on operand set i % len(sets),
+    so no launch finds its A, B or C in the MALL or the L2s."""
+    import torch
+    n = len(sets)
+    fns = [make_step(*s) for s in sets]
+    for i in range(2 * n):
+        fns[i % n]()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        fns[i % n]()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def cpu_threads():
@@ -196,6 +252,8 @@ def main():
     ap.add_argument("--warm-seconds", type=float, default=3.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-blaslt", action="store_true")
+    ap.add_argument("--no-cold", action="store_true")
+    ap.add_argument("--allow-partitioned", action="store_true")
     ap.add_argument("--mode", default="gemm", choices=["gemm", "copy"])
     args = ap.parse_args()
 
@@ -210,6 +268,7 @@ def main():
     if args.mode == "copy":
         run_copy_mode(max(args.steps, 1))
         return
+    device = device_check(args.allow_partitioned)
 
     from ridge_amd import gemm as G
 
@@ -270,6 +329,48 @@ def main():
         blas_after = flops * args.steps / (ms * 1e-3) / 1e12
         blas.close()
 
+    # Cold: the same launches rotated over operand sets that together exceed
+    # twice the MALL, so every launch streams A and B from HBM (and writes C to
+    # lines no cache holds). The warm figure above re-uses one set, as the
+    # reference's timing loop does (measure.cu:111-150).
+    cold = None
+    if not args.no_cold:
+        set_bytes = 2 * (M * K + K * N + M * N)
+        n_sets = cold_sets(set_bytes)
+        sets = [(A, B, C)]
+        for i in range(1, n_sets):
+            Ai = torch.empty_like(A)
+            Bi = torch.empty_like(B)
+            G.fill_uniform(Ai, 1)
+            G.fill_uniform(Bi, 2)
+            sets.append((Ai, Bi, torch.empty_like(C)))
+        torch.cuda.synchronize()
+
+        def make_step(a, b, c):
+            def f():
+                rc = G.launch(idx, a, b, c, M, N, K, stream)
+                if rc != 0:
+                    raise SystemExit("ridge_gemm_launch returned %d" % rc)
+            return f
+
+        cold_steps = max(args.steps // 4, 4 * n_sets)
+        cold_ms = time_cold(make_step, sets, cold_steps, stream)
+        cold = {"tflops": round(flops / (cold_ms * 1e-3) / 1e12, 3), "ms_per_launch": round(cold_ms, 6),
+                "sets": n_sets, "set_bytes": set_bytes, "launches": cold_steps,
+                "roofline": roofline(M, N, K, cold_ms, None)}
+        if blas is not None:
+            blas = G.BlasLt()
+            blas.prepare(A, B, C, M, N, K, candidates=16, iters=20, stream=stream)
+
+            def make_blas_step(a, b, c):
+                return lambda: blas.gemm(a, b, c, M, N, K, stream=stream)
+
+            blas_cold_ms = time_cold(make_blas_step, sets, cold_steps, stream)
+            blas.close()
+            cold["hipblaslt_tflops"] = round(flops / (blas_cold_ms * 1e-3) / 1e12, 3)
+            cold["frac_of_hipblaslt"] = round(blas_cold_ms / cold_ms, 4)
+        del sets
+
     traffic = measured_traffic(M, N, K, key)
 
     out = {
@@ -297,6 +398,9 @@ def main():
                             "after": round(blas_after, 3),
                             "drift": round(abs(blas_after - blas_before) / blas_before, 4),
                             "frac_of_hipblaslt": round(value / best, 4)}
+    if cold is not None:
+        out["cold"] = cold
+    out["device"] = device
     out["autotune"] = autotune_regret(10)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)

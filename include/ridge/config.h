@@ -41,6 +41,12 @@ struct GemmConfig {
     // launch-order reuse model (HardwareModel::l2ReuseModel 2) reads it; the
     // reference model has no such field.
     int groupM = 8;
+
+    // Kernel schedule of the row: -1 derives it from the tile (two waves per
+    // SIMD with >= 3 stages is ping-pong, anything else uniform), 0 uniform,
+    // 1 ping-pong, 2 persistent store-behind. Only HardwareModel::persistentModel
+    // 1 reads the value 2; the reference model has no such field.
+    int schedule = -1;
 };
 
 }  // namespace ridge

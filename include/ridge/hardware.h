@@ -53,6 +53,11 @@ struct HardwareModel {
     int pingPongModel = 0;           // 0: operand reads in series with the MFMAs (reference)
                                      // 1: a workgroup of 2 waves per SIMD with >= 3 stages runs
                                      //    the ping-pong schedule: reads overlap the MFMAs
+    int persistentModel = 0;         // 0: every row is a one-tile-per-workgroup kernel (reference)
+                                     // 1: schedule-2 rows are persistent: two loader waves and
+                                     //    the epilogue staging join the workgroup, which walks
+                                     //    ceil(tiles / slots) tiles and pays one fill and one
+                                     //    drain for all of them
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -50,7 +50,11 @@ typedef struct ridge_gemm_variant {
     int sgprs;           /* scalar registers per wave */
     int scratchBytes;    /* private segment bytes per lane (0 = no spills) */
     int occupancy;       /* waves per SIMD the compiler reports */
-    int pingPong;        /* 1: ping-pong schedule (8 wavefronts, >= 3 stages); 0: uniform */
+    int pingPong;        /* 1: ping-pong schedule (8 wavefronts, >= 3 stages); 0: otherwise */
+    int schedule;        /* 0: uniform, 1: ping-pong, 2: persistent store-behind (one workgroup
+                            per CU slot walks output tiles; two loader wavefronts feed the ring,
+                            so `waves` and `threads` count them and `ldsBytes` includes the
+                            epilogue staging) */
 } ridge_gemm_variant_t;
 
 /* Number of rows in the table (the reference's numVariants(), gemm-mma.cu:121). */

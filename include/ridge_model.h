@@ -27,6 +27,8 @@ typedef struct ridge_model_config {
     int stages;
     int regsPerThread;      /* 0 = unknown */
     int groupM;             /* launch-order group size along M (read by l2ReuseModel 2 only) */
+    int schedule;           /* -1: from the tile, 0 uniform, 1 ping-pong, 2 persistent
+                               (2 is read by persistentModel 1 only) */
 } ridge_model_config_t;
 
 typedef struct ridge_model_prediction {

@@ -124,6 +124,7 @@ def hardware_json(res, spec, arch):
         "l2ReuseModel": 2,
         "prologueModel": 1,
         "pingPongModel": 1,
+        "persistentModel": 1,
         "warpsNeededToHideIlp8": res.get("warpsNeededToHideIlp8", 0.0),
         "nominalClockHz": res.get("nominalClockHz", spec["clock_hz"]),
         "impliedPeakTflops": res["impliedPeakTflops"],

@@ -18,10 +18,49 @@ namespace {
 
 typedef hipError_t (*LaunchFn)(const void*, const void*, void*, int, int, int, hipStream_t);
 
-// Schedule choice, a function of the tile config: eight wavefronts (two per
-// SIMD) with a ring of three or more stages run the ping-pong schedule, every
-// other variant the uniform one.
+// Schedules (ridge_gemm_variant_t.schedule). Rows written RIDGE_VARIANT take
+// theirs from the tile config: eight wavefronts (two per SIMD) with a ring of
+// three or more stages run the ping-pong schedule, every other row the uniform
+// one. Rows written RIDGE_VARIANT_PERSISTENT run the persistent store-behind
+// schedule.
+enum Schedule { kUniform = 0, kPingPong = 1, kPersistent = 2 };
 constexpr bool usesPingPong(int waves, int stages) { return waves == 8 && stages >= 3; }
+
+// Workgroups of `kernel` resident on the current device at once (CUs x
+// workgroups per CU), cached per device: the persistent grid. The host side is
+// single-threaded, as the reference's (the table is an immutable static).
+int residentSlots(const void* kernel, int threads, int& cache) {
+    if (cache > 0) return cache;
+    int dev = 0, cus = 0, perCu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, kernel, threads, 0) != hipSuccess) return 0;
+    cache = cus * (perCu > 0 ? perCu : 1);
+    return cache;
+}
+
+constexpr int kMaxDevices = 64;
+
+template <int BM, int BN, int BK, int WM, int WN, int S, int G>
+hipError_t launchPersistent(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t stream) {
+    using P = ridge::PersistentTraits<BM, BN, BK, WM, WN, S, G>;
+    static int slots[kMaxDevices];
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    const void* kernel = reinterpret_cast<const void*>(&ridge::gemmMfmaPersistentKernel<BM, BN, BK, WM, WN, S, G>);
+    const int resident = residentSlots(kernel, P::kThreads, slots[dev]);
+    if (resident <= 0) return hipErrorInvalidConfiguration;
+    // Every workgroup must own at least one tile (the kernel's tile count per
+    // workgroup assumes it).
+    const int tiles = (M / BM) * (N / BN);
+    const dim3 grid((unsigned)(tiles < resident ? tiles : resident));
+    hipLaunchKernelGGL((ridge::gemmMfmaPersistentKernel<BM, BN, BK, WM, WN, S, G>), grid, dim3(P::kThreads), 0,
+                       stream, static_cast<const _Float16*>(A), static_cast<const _Float16*>(B),
+                       static_cast<_Float16*>(C), M, N, K);
+    return hipGetLastError();
+}
 
 template <int BM, int BN, int BK, int WM, int WN, int S, int G>
 hipError_t launchVariant(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t stream) {
@@ -45,7 +84,7 @@ struct Entry {
     int ldsBytes;
     int threads;
     int waves;
-    int pingPong;
+    int schedule;
     LaunchFn launch;
 };
 
@@ -54,13 +93,24 @@ struct Entry {
           ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kLdsBytes,                            \
           ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kThreads,                             \
           ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kWaves,                               \
-          usesPingPong(ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kWaves, S) ? 1 : 0,       \
+          usesPingPong(ridge::GemmTraits<BM, BN, BK, WM, WN, S, G>::kWaves, S) ? kPingPong : kUniform, \
           &launchVariant<BM, BN, BK, WM, WN, S, G>},
+
+// ldsBytes includes the epilogue staging; threads and waves include the two
+// loader wavefronts.
+#define RIDGE_VARIANT_PERSISTENT(BM, BN, BK, WM, WN, S, G)                                   \
+    Entry{BM, BN, BK, WM, WN, S, G,                                                          \
+          ridge::PersistentTraits<BM, BN, BK, WM, WN, S, G>::kLdsBytes,                      \
+          ridge::PersistentTraits<BM, BN, BK, WM, WN, S, G>::kThreads,                       \
+          ridge::PersistentTraits<BM, BN, BK, WM, WN, S, G>::kWaves,                         \
+          kPersistent,                                                                       \
+          &launchPersistent<BM, BN, BK, WM, WN, S, G>},
 
 const Entry kTable[] = {
 #include "gemm_variants.def"
 };
 #undef RIDGE_VARIANT
+#undef RIDGE_VARIANT_PERSISTENT
 
 constexpr int kNumVariants = int(sizeof(kTable) / sizeof(kTable[0]));
 
@@ -79,7 +129,9 @@ int ridge_gemm_get_variant(int i, ridge_gemm_variant_t* out) {
     std::memset(&v, 0, sizeof(v));
     v.BM = e.BM; v.BN = e.BN; v.BK = e.BK; v.WM = e.WM; v.WN = e.WN;
     v.stages = e.stages; v.groupM = e.groupM;
-    v.ldsBytes = e.ldsBytes; v.threads = e.threads; v.waves = e.waves; v.pingPong = e.pingPong;
+    v.ldsBytes = e.ldsBytes; v.threads = e.threads; v.waves = e.waves;
+    v.pingPong = e.schedule == kPingPong ? 1 : 0;
+    v.schedule = e.schedule;
     if (i < ridge_gemm_resource_count) {
         const ridge_gemm_resources_t& r = ridge_gemm_resource_table[i];
         v.vgprs = r.vgprs; v.agprs = r.agprs; v.sgprs = r.sgprs;
@@ -123,14 +175,14 @@ int ridge_gemm_launch(int i, const void* A, const void* B, void* C, int M, int N
 
 size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {
     std::string s = "idx,BM,BN,BK,WM,WN,stages,groupM,ldsBytes,threads,regsPerThread,waves,vgprs,agprs,sgprs,"
-                    "scratchBytes,occupancy,pingPong\n";
+                    "scratchBytes,occupancy,pingPong,schedule\n";
     char line[256];
     for (int i = 0; i < kNumVariants; ++i) {
         ridge_gemm_variant_t v;
         ridge_gemm_get_variant(i, &v);
-        std::snprintf(line, sizeof(line), "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d\n", i, v.BM, v.BN,
-                      v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes, v.threads, v.regsPerThread, v.waves,
-                      v.vgprs, v.agprs, v.sgprs, v.scratchBytes, v.occupancy, v.pingPong);
+        std::snprintf(line, sizeof(line), "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d\n", i, v.BM,
+                      v.BN, v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes, v.threads, v.regsPerThread, v.waves,
+                      v.vgprs, v.agprs, v.sgprs, v.scratchBytes, v.occupancy, v.pingPong, v.schedule);
         s += line;
     }
     if (buf != nullptr && cap > 0) {
@@ -143,7 +195,7 @@ size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {
 
 const char* ridge_gemm_build_info(void) {
     return "ridge_gemm gfx950 mfma_f32_16x16x32_f16, direct-to-LDS ring, tr16 B reads, xcd+groupM order, "
-           "ping-pong schedule for 8-wave rings of 3+ stages";
+           "ping-pong schedule for 8-wave rings of 3+ stages, persistent store-behind rows with loader waves";
 }
 
 }  // extern "C"

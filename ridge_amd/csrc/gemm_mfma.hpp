@@ -116,6 +116,20 @@ __device__ __forceinline__ int xcdRemap(int pid, int n) {
     return x * q + (x < r ? x : r) + pid / kXcds;
 }
 
+// GroupM launch order: logical id pid -> (row, column) of the output tile's
+// first element. Groups of GROUPM tile rows are walked column by column, so
+// consecutive ids share B column panels and a group shares A row panels.
+template <int BM, int BN, int GROUPM>
+__device__ __forceinline__ void tileOf(int pid, int M, int N, int& row, int& col) {
+    const int numPidM = M / BM;
+    const int numPidN = N / BN;
+    const int pidInGroup = pid % (GROUPM * numPidN);
+    const int firstPidM = (pid / (GROUPM * numPidN)) * GROUPM;
+    const int groupRows = min(numPidM - firstPidM, GROUPM);
+    row = (firstPidM + pidInGroup % groupRows) * BM;
+    col = (pidInGroup / groupRows) * BN;
+}
+
 // Direct-to-LDS 16-byte load: lane t of the wave writes LDS bytes
 // [ldsAddr + 16 t, +16) with the 16 bytes at base + offset. base and ldsAddr are
 // wave-uniform (scalar registers; ldsAddr is carried in M0), offset is the lane's
@@ -205,6 +219,75 @@ __device__ __forceinline__ void staticFor(F&& f) {
     staticForImpl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Epilogue of one wave through a private LDS region. In the MFMA layout a lane
+// holds four consecutive columns of one row, so direct stores are 8 bytes wide
+// and one wave instruction touches 16 rows x 32 bytes; at small K, where writing
+// C is the whole cost, that pattern runs at 2.9 TB/s against 4.1 TB/s for
+// full-row 16-byte stores. So the wave converts its TM x TN tiles to FP16
+// (nearest even), writes EPI 16-row tile-rows at a time into `region`
+// (16 * EPI * WN * 2 bytes) and reads them back row by row: every lane then
+// stores 16 contiguous bytes and one instruction covers 64 / (WN / 8) complete
+// rows of the wave tile. Row r of the region keeps its chunks XOR-permuted by
+// (r * CPR / 16) % CPR: the 8-byte writes (16 rows at one chunk per 32 lanes)
+// and the 16-byte reads (8 lanes along a row) are both conflict-free. Up to 8
+// read-backs are in flight before their stores issue. The global stores are
+// not waited for; NT marks them non-temporal (streamed past the caches), which
+// lifts a C-bound kernel's write rate when C is not re-read soon.
+template <int TM, int TN, int WN, int EPI, bool NT>
+__device__ __forceinline__ void storeStaged(const float4_t (&acc)[TM][TN], RIDGE_LDS_AS char* region,
+                                            _Float16* cWave, int N, int lane) {
+    constexpr int CPR = WN / 8;            // 16-byte chunks per wave-tile row
+    constexpr int kRowsPerStore = 64 / CPR;
+    constexpr int kStores = 16 * EPI / kRowsPerStore;   // store instructions per pass
+    constexpr int kBatch = kStores < 8 ? kStores : 8;
+    static_assert(TM % EPI == 0, "passes must cover the wave tile");
+    static_assert(kStores % kBatch == 0, "read-back batches must cover the pass");
+    auto swz = [](int row, int chunk) { return chunk ^ ((row * CPR / 16) % CPR); };
+    const int g = lane / 16;
+    const int r16 = lane % 16;
+    staticFor<TM / EPI>([&](auto passC) {
+        constexpr int tm0 = passC.value * EPI;
+#pragma unroll
+        for (int i = 0; i < EPI; ++i) {
+            const int row = 16 * i + r16;
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                const int col = tn * kMfmaN + 4 * g;
+                half4_t v;
+                v[0] = (_Float16)acc[tm0 + i][tn][0];
+                v[1] = (_Float16)acc[tm0 + i][tn][1];
+                v[2] = (_Float16)acc[tm0 + i][tn][2];
+                v[3] = (_Float16)acc[tm0 + i][tn][3];
+                *(RIDGE_LDS_AS half4_t*)(region + (row * CPR + swz(row, col / 8)) * 16 + (col % 8) * 2) = v;
+            }
+        }
+        // The region was written by this wave only; wait for the writes
+        // before reading them back.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int j0 = 0; j0 < kStores; j0 += kBatch) {
+            half8_t v[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int row = (j0 + j) * kRowsPerStore + lane / CPR;
+                v[j] = *(const RIDGE_LDS_AS half8_t*)(region + (row * CPR + swz(row, lane % CPR)) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int row = (j0 + j) * kRowsPerStore + lane / CPR;
+                half8_t* dst = (half8_t*)(cWave + (size_t)(16 * tm0 + row) * N + 8 * (lane % CPR));
+                if constexpr (NT) {
+                    __builtin_nontemporal_store(v[j], dst);
+                } else {
+                    *dst = v[j];
+                }
+            }
+        }
+        // The next pass rewrites the region: its reads must have returned.
+        if (passC.value + 1 < TM / EPI) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    });
+}
+
 // Per-workgroup state and the operations both schedules are built from: the
 // output tile, the direct-to-LDS refill of a stage, the fragment reads of a
 // k-step, the MFMAs of a k-step and the epilogue.
@@ -221,6 +304,8 @@ struct GemmBlock {
     uint32_t ldsBase;     // its LDS byte address (scalar)
     int lane, wave, waveM, waveN;
     int blockRow, blockCol;
+    const _Float16* baseA;
+    const _Float16* baseB;
     const char* gA;       // A + blockRow * K (bytes), scalar
     const char* gB;       // B + blockCol (bytes), scalar
     size_t tileStrideB;   // bytes between K tiles of B: BK * N * 2
@@ -240,18 +325,9 @@ struct GemmBlock {
         waveM = wave / T::kWavesN;
         waveN = wave % T::kWavesN;
 
-        // XCD remap, then the GroupM launch order (reference gemm-mma.cuh:158-178).
-        const int numPidM = M / BM;
-        const int numPidN = N / BN;
-        const int pid = xcdRemap(blockIdx.x, gridDim.x);
-        const int pidInGroup = pid % (GROUPM * numPidN);
-        const int firstPidM = (pid / (GROUPM * numPidN)) * GROUPM;
-        const int groupRows = min(numPidM - firstPidM, GROUPM);
-        blockRow = (firstPidM + pidInGroup % groupRows) * BM;
-        blockCol = (pidInGroup / groupRows) * BN;
-
-        gA = reinterpret_cast<const char*>(A + (size_t)blockRow * K);
-        gB = reinterpret_cast<const char*>(B + blockCol);
+        baseA = A;
+        baseB = B;
+        setTile(xcdRemap(blockIdx.x, gridDim.x), M, N, K);
         tileStrideB = (size_t)BK * N * 2;
         // Wave instruction j fills physical chunks [64 j, 64 j + 64) of a tile;
         // lane t's chunk holds logical chunk swizzle(64 j + t).
@@ -293,6 +369,14 @@ struct GemmBlock {
             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[tm][tn][e] = 0.0f;
+    }
+
+    // The output tile of logical launch id `pid` (after the XCD remap) in the
+    // GroupM launch order (reference gemm-mma.cuh:158-178), and its operand bases.
+    __device__ __forceinline__ void setTile(int pid, int M, int N, int K) {
+        tileOf<BM, BN, GROUPM>(pid, M, N, blockRow, blockCol);
+        gA = reinterpret_cast<const char*>(baseA + (size_t)blockRow * K);
+        gB = reinterpret_cast<const char*>(baseB + blockCol);
     }
 
     // Refills LDS stage `stage` with K tile kTile (this wave's share). No vector
@@ -339,19 +423,10 @@ struct GemmBlock {
                 acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
     }
 
-    // Epilogue through LDS. In the MFMA layout a lane holds four consecutive
-    // columns of one row, so direct stores are 8 bytes wide and one wave
-    // instruction touches 16 rows x 32 bytes; at small K, where writing C is the
-    // whole cost, that pattern runs at 2.9 TB/s against 4.1 TB/s for full-row
-    // 16-byte stores. So each wave converts its tile to FP16 (nearest even),
-    // writes it into a private LDS region and reads it back row by row: every
-    // lane then stores 16 contiguous bytes and one instruction covers 64/CPR_C
-    // complete rows of the wave tile. Regions are per wave, so the only
-    // cross-wave hazard is the ring: every wave must be past its last ring read
-    // (a barrier) before the call. Waves whose whole tile does not fit the ring
-    // at once make several passes of kEpiTiles 16-row tile-rows.
-    static constexpr int CPR_C = WN / 8;           // 16-byte chunks per wave-tile row
-    static constexpr int kRowsPerStore = 64 / CPR_C;
+    // Epilogue through LDS (storeStaged below). Regions are per wave, so the
+    // only cross-wave hazard is the ring they overlay: every wave must be past
+    // its last ring read (a barrier) before the call. Waves whose whole tile does
+    // not fit the ring at once make several passes of kEpiTiles 16-row tile-rows.
     static constexpr int epiTiles() {
         int p = TM;
         while (p > 1 && (TM % p != 0 || T::kWaves * 16 * p * WN * 2 > T::kLdsBytes)) --p;
@@ -361,47 +436,16 @@ struct GemmBlock {
     static constexpr int kEpiRegionBytes = 16 * kEpiTiles * WN * 2;
     static_assert(T::kWaves * kEpiRegionBytes <= T::kLdsBytes, "epilogue regions must fit the ring");
 
-    // Row r of a region keeps its chunks XOR-permuted by (r * CPR_C / 16) % CPR_C:
-    // the 8-byte writes (16 rows at one chunk per 32 lanes) and the 16-byte reads
-    // (8 lanes along a row) are both conflict-free.
-    __device__ __forceinline__ static int swizzleC(int row, int chunk) {
-        return chunk ^ ((row * CPR_C / 16) % CPR_C);
+    // This wave's sub-tile of C (row-major, leading dimension N).
+    __device__ __forceinline__ _Float16* waveC(_Float16* C, int N) const {
+        return C + (size_t)(blockRow + waveM * WM) * N + blockCol + waveN * WN;
     }
 
+    // Regular (cached) stores: these kernels are timed, like the reference's,
+    // on operands re-used across launches, where C stays in the MALL.
     __device__ __forceinline__ void store(_Float16* C, int N) const {
         RIDGE_LDS_AS char* region = (RIDGE_LDS_AS char*)(const_cast<char*>(lds)) + wave * kEpiRegionBytes;
-        const int g = lane / 16;
-        const int r16 = lane % 16;
-        _Float16* cWave = C + (size_t)(blockRow + waveM * WM) * N + blockCol + waveN * WN;
-        staticFor<TM / kEpiTiles>([&](auto passC) {
-            constexpr int tm0 = passC.value * kEpiTiles;
-#pragma unroll
-            for (int i = 0; i < kEpiTiles; ++i) {
-                const int row = 16 * i + r16;
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
-                    const int col = tn * kMfmaN + 4 * g;
-                    half4_t v;
-                    v[0] = (_Float16)acc[tm0 + i][tn][0];
-                    v[1] = (_Float16)acc[tm0 + i][tn][1];
-                    v[2] = (_Float16)acc[tm0 + i][tn][2];
-                    v[3] = (_Float16)acc[tm0 + i][tn][3];
-                    *(RIDGE_LDS_AS half4_t*)(region + (row * CPR_C + swizzleC(row, col / 8)) * 16 + (col % 8) * 2) = v;
-                }
-            }
-            // The region was written by this wave only; wait for the writes
-            // before reading them back.
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int j = 0; j < 16 * kEpiTiles / kRowsPerStore; ++j) {
-                const int row = j * kRowsPerStore + lane / CPR_C;
-                const int chunk = lane % CPR_C;
-                const half8_t v = *(const RIDGE_LDS_AS half8_t*)(region + (row * CPR_C + swizzleC(row, chunk)) * 16);
-                *(half8_t*)(cWave + (size_t)(16 * tm0 + row) * N + 8 * chunk) = v;
-            }
-            // The next pass rewrites the region: its reads must have returned.
-            if (passC.value + 1 < TM / kEpiTiles) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        });
+        storeStaged<TM, TN, WN, kEpiTiles, false>(acc, region, waveC(C, N), N, lane);
     }
 };
 
@@ -590,6 +634,196 @@ void gemmMfmaPingPongKernel(const _Float16* __restrict__ A, const _Float16* __re
     // past its last ring read, and the epilogue may reuse LDS.
     if (group == 0) barrierLds();
     blk.store(C, N);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent store-behind schedule, for shapes whose cost is writing C (small K).
+//
+// One workgroup per CU walks the output tiles r, r + grid, r + 2 grid, ... of
+// its logical id r (XCD remap, then GroupM order, as above), so at round j each
+// XCD works on a compact block of 32 tiles. The workgroup has two kinds of
+// wavefronts:
+//  * compute waves 0 .. kWaves-1 (the tile's wave grid) read fragments, run the
+//    MFMAs and, after a tile's last K tile, convert and store it through a
+//    private LDS staging region (storeStaged). They issue no global loads, so
+//    their global stores are never waited for: a tile's C drains to memory
+//    while the next tile is loaded and multiplied.
+//  * loader waves kWaves .. kWaves+kLoaders-1 only issue direct-to-LDS loads.
+//    They stream the workgroup's K tiles, in order across output tiles, into
+//    an LDS ring of STAGES buffers, and each waits on its own vmcnt, which
+//    holds nothing but its loads.
+// (On gfx9 one wave's loads and stores share vmcnt and may complete out of
+// order, so a wave that both prefetches and stores cannot wait for a load
+// without draining its stores; the split keeps the two streams in different
+// waves.)
+//
+// With g = 0, 1, ... the workgroup's K tiles in order, barrier B_g separates
+// the compute waves' last reads of K tile g-1 from their first reads of K tile
+// g. The loader arrives at B_g only once K tile g is in LDS, and after B_g
+// refills the stage of K tile g-1 with K tile g+STAGES-1. Every wave executes
+// B_0 .. B_{G-1}, G barriers in all.
+// ---------------------------------------------------------------------------
+constexpr int kPersistentLoaders = 2;
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUPM>
+struct PersistentTraits {
+    using T = GemmTraits<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    static constexpr int kLoaders = kPersistentLoaders;
+    static constexpr int kWaves = T::kWaves + kLoaders;
+    static constexpr int kThreads = kWaves * kWaveSize;
+    static constexpr int kLoadsA = T::kInstA / kLoaders;   // per loader wave per K tile
+    static constexpr int kLoadsB = T::kInstB / kLoaders;
+    static constexpr int kLoads = kLoadsA + kLoadsB;
+    // Staging: the largest number of 16-row tile-rows per pass that fits
+    // beside the ring.
+    static constexpr int epiTiles() {
+        int p = T::kTilesM;
+        while (p > 1 && (T::kTilesM % p != 0 || T::kLdsBytes + T::kWaves * 16 * p * WN * 2 > 163840)) --p;
+        return p;
+    }
+    static constexpr int kEpiTiles = epiTiles();
+    static constexpr int kRegionBytes = 16 * kEpiTiles * WN * 2;
+    static constexpr int kLdsBytes = T::kLdsBytes + T::kWaves * kRegionBytes;
+    static_assert(T::kInstA % kLoaders == 0 && T::kInstB % kLoaders == 0, "loads must split over the loaders");
+    static_assert((STAGES - 1) * kLoads < 64, "a loader's in-flight loads exceed the vmcnt counter");
+    static_assert(kLdsBytes <= 163840, "ring and staging exceed the 160 KiB of LDS");
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int GROUPM>
+__global__ __launch_bounds__(((BM / WM) * (BN / WN) + kPersistentLoaders) * kWaveSize)
+void gemmMfmaPersistentKernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                              _Float16* __restrict__ C, int M, int N, int K) {
+    using T = GemmTraits<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    using P = PersistentTraits<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    using Blk = GemmBlock<BM, BN, BK, WM, WN, STAGES, GROUPM>;
+    constexpr int TM = T::kTilesM;
+    constexpr int TN = T::kTilesN;
+    constexpr int KS = T::kSteps;
+    constexpr int L = P::kLoads;
+
+    __shared__ __attribute__((aligned(1024))) char lds[P::kLdsBytes];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+    const int lane = threadIdx.x % kWaveSize;
+    const int grid = gridDim.x;
+    const int self = xcdRemap(blockIdx.x, grid);
+    const int numTiles = (M / BM) * (N / BN);
+    const int numK = K / BK;
+    // The launcher makes grid <= numTiles, so every workgroup has a tile.
+    const int G = ((numTiles - self + grid - 1) / grid) * numK;
+
+    if (wave >= T::kWaves) {
+        // Loader wave l issues wave instructions l, l + kLoaders, ... of each
+        // tile; instruction j fills physical chunks [64 j, 64 j + 64).
+        const int l = wave - T::kWaves;
+        const uint32_t ldsBase = ldsAddress(lds);
+        uint32_t offA[P::kLoadsA], offB[P::kLoadsB];
+#pragma unroll
+        for (int i = 0; i < P::kLoadsA; ++i) {
+            const int q = swizzleA((i * P::kLoaders + l) * 64 + lane);
+            offA[i] = (uint32_t)(((q / T::kChunksPerRowA) * K + (q % T::kChunksPerRowA) * 8) * 2);
+        }
+#pragma unroll
+        for (int i = 0; i < P::kLoadsB; ++i) {
+            const int q = swizzleB<T::kChunksPerRowB>((i * P::kLoaders + l) * 64 + lane);
+            offB[i] = (uint32_t)(((q / T::kChunksPerRowB) * N + (q % T::kChunksPerRowB) * 8) * 2);
+        }
+        // K tiles are issued strictly in order, so a cursor (output tile, K
+        // tile) replaces per-issue index arithmetic.
+        int curTile = 0, curK = 0, row, col;
+        tileOf<BM, BN, GROUPM>(self, M, N, row, col);
+        const char* srcA = reinterpret_cast<const char*>(A + (size_t)row * K);
+        const char* srcB = reinterpret_cast<const char*>(B + col);
+        const size_t strideB = (size_t)BK * N * 2;
+        auto issueNext = [&](int stage) {
+            const uint32_t dstA = ldsBase + stage * T::kBytesA;
+            const uint32_t dstB = ldsBase + T::kRegionA + stage * T::kBytesB;
+#pragma unroll
+            for (int i = 0; i < P::kLoadsA; ++i)
+                globalLoadLds16(srcA, offA[i], dstA + (i * P::kLoaders + l) * 1024);
+#pragma unroll
+            for (int i = 0; i < P::kLoadsB; ++i)
+                globalLoadLds16(srcB, offB[i], dstB + (i * P::kLoaders + l) * 1024);
+            srcA += BK * 2;
+            srcB += strideB;
+            if (++curK == numK && ++curTile * numK < G) {
+                curK = 0;
+                tileOf<BM, BN, GROUPM>(self + curTile * grid, M, N, row, col);
+                srcA = reinterpret_cast<const char*>(A + (size_t)row * K);
+                srcB = reinterpret_cast<const char*>(B + col);
+            }
+        };
+        staticFor<STAGES - 1>([&](auto sC) {
+            if (sC.value < G) issueNext(sC.value);
+        });
+        if (G >= STAGES - 1) {
+            waitVmcnt<(STAGES - 2) * L>();
+        } else {
+            waitVmcnt<0>();
+        }
+        barrierLds();  // B_0
+        for (int g0 = 0; g0 < G; g0 += STAGES) {
+            staticFor<STAGES>([&](auto sC) {
+                constexpr int s = sC.value;
+                const int g = g0 + s;
+                if (g + 1 < G) {
+                    // Past B_g: the stage of K tile g-1 is free.
+                    if (g + STAGES - 1 < G) {
+                        issueNext((s + STAGES - 1) % STAGES);  // K tile g+STAGES-1
+                        waitVmcnt<(STAGES - 2) * L>();
+                    } else {
+                        waitVmcnt<0>();
+                    }
+                    barrierLds();  // B_{g+1}: K tile g+1 is in LDS
+                }
+            });
+        }
+        return;
+    }
+
+    Blk blk(lds, A, B, M, N, K);
+    RIDGE_LDS_AS char* region = (RIDGE_LDS_AS char*)(lds) + T::kLdsBytes + wave * P::kRegionBytes;
+    barrierLds();  // B_0
+    half8_t fa[2][TM];
+    half8_t fb[2][TN];
+    blk.template readFrags<0>(0, fa[0], fb[0]);
+    int kt = 0;
+    int tile = 0;
+    constexpr int U = (STAGES * KS) % 2 == 0 ? STAGES : 2 * STAGES;
+    for (int g0 = 0; g0 < G; g0 += U) {
+        staticFor<U>([&](auto iC) {
+            constexpr int i = iC.value;
+            constexpr int s = i % STAGES;
+            constexpr int sNext = (s + 1) % STAGES;
+            const int g = g0 + i;
+            if (g < G) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int cur = (i * KS + ks) & 1;
+                    if (ks + 1 < KS) {
+                        blk.template readFrags<s>(ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                    } else if (g + 1 < G) {
+                        barrierLds();  // B_{g+1}
+                        blk.template readFrags<sNext>(0, fa[cur ^ 1], fb[cur ^ 1]);
+                    }
+                    blk.mfmaStep(fa[cur], fb[cur]);
+                    interleaveHint<TM, TN>();
+                }
+                if (++kt == numK) {
+                    blk.setTile(self + tile * grid, M, N, K);
+                    // Non-temporal: measured +21% cold and +1% warm at 8192^2 x 128.
+                    storeStaged<TM, TN, WN, P::kEpiTiles, true>(blk.acc, region, blk.waveC(C, N), N, lane);
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) blk.acc[tm][tn][e] = 0.0f;
+                    kt = 0;
+                    ++tile;
+                }
+            }
+        });
+    }
 }
 
 }  // namespace ridge

@@ -66,6 +66,7 @@ HardwareModel HardwareModel::mi355x() {
     h.l2ReuseModel = 2;
     h.prologueModel = 1;
     h.pingPongModel = 1;
+    h.persistentModel = 1;
     return h;
 }
 
@@ -218,6 +219,7 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
         !optionalInteger(kv, "l2ReuseModel", h.l2ReuseModel, err) ||
         !optionalInteger(kv, "prologueModel", h.prologueModel, err) ||
         !optionalInteger(kv, "pingPongModel", h.pingPongModel, err) ||
+        !optionalInteger(kv, "persistentModel", h.persistentModel, err) ||
         !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
         err = path + ": " + err;
         return false;

@@ -27,6 +27,11 @@
 //                           tiles the kernel actually issues     (reference :91-98)
 //   latency hiding        = hw.warpsNeededToHideIlp8 when a wave carries >= 8
 //                           independent accumulator chains      (reference :72-74)
+//   persistent rows       = hw.persistentModel 1 and cfg.schedule 2: two loader
+//                           waves and the epilogue staging join the workgroup,
+//                           which walks ceil(tiles / slots) tiles and pays one
+//                           fill and one drain for all of them (reference: one
+//                           tile per workgroup, :91-99)
 //
 // With the defaults (a100() or a reference JSON) every term reduces to the
 // reference's expression in the same double-precision operation order, so the
@@ -69,6 +74,21 @@ MmaShape mmaShapeFor(DType dtype, const HardwareModel& hw) {
 
 namespace {
 
+// Loader wavefronts of a persistent workgroup (the kernels' PersistentTraits).
+constexpr int kPersistentLoaderWaves = 2;
+
+// LDS of a persistent workgroup's epilogue staging: each compute wave stages
+// the largest number of 16-row tile-rows that divides its tile-rows and fits
+// beside the ring (the kernels' PersistentTraits::epiTiles).
+double persistentStagingBytes(const GemmConfig& cfg, const HardwareModel& hw, int computeWaves, double ringBytes,
+                              int db) {
+    const int tileRows = cfg.warpM / cfg.mmaM;
+    int p = tileRows;
+    auto bytes = [&](int q) { return double(computeWaves) * cfg.mmaM * q * cfg.warpN * db; };
+    while (p > 1 && (tileRows % p != 0 || ringBytes + bytes(p) > double(hw.smemBytesPerSM))) --p;
+    return bytes(p);
+}
+
 // Workgroups per CU allowed by the register file.
 double workgroupsByRegisters(const GemmConfig& cfg, const HardwareModel& hw, int numWarps, int threadsPerCta) {
     if (cfg.regsPerThread <= 0) return 1e9;
@@ -100,7 +120,11 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     Prediction p;
 
     const int numWarps = (cfg.BM / cfg.warpM) * (cfg.BN / cfg.warpN);
-    const int threadsPerCta = numWarps * hw.waveSize;
+    // A persistent row's loader waves take wave slots and registers but issue
+    // no matrix instructions and no operand reads.
+    const bool persistent = hw.persistentModel == 1 && cfg.schedule == 2;
+    const int residentWarps = persistent ? numWarps + kPersistentLoaderWaves : numWarps;
+    const int threadsPerCta = residentWarps * hw.waveSize;
     p.numWarps = numWarps;
 
     // Per K-step times of one workgroup: matrix instructions, and the operand
@@ -115,8 +139,8 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // The ping-pong schedule (two waves per SIMD, a ring of three or more stages)
     // runs one wave's operand reads under the other wave's MFMAs, so a K-step
     // costs the longer of the two instead of their sum.
-    const bool pingPong = hw.pingPongModel == 1 && hw.simdsPerSM > 0 &&
-                          numWarps == 2 * hw.simdsPerSM && cfg.stages >= 3;
+    const bool derivedPingPong = hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM && cfg.stages >= 3;
+    const bool pingPong = hw.pingPongModel == 1 && (cfg.schedule < 0 ? derivedPingPong : cfg.schedule == 1);
     const double tStep = pingPong ? std::max(tCompute, tSmem) : tCompute + tSmem;
     const double smEfficiency = tCompute / tStep;
     p.tComputeCycles = tCompute;
@@ -125,10 +149,12 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     p.smEfficiency = smEfficiency;
 
     // Occupancy: the tightest of LDS, wave slots, registers and the workgroup cap.
-    const double smemBytesPerCta = double(cfg.stages) * (cfg.BM * cfg.BK + cfg.BK * cfg.BN) * db;
+    const double ringBytes = double(cfg.stages) * (cfg.BM * cfg.BK + cfg.BK * cfg.BN) * db;
+    const double smemBytesPerCta =
+        persistent ? ringBytes + persistentStagingBytes(cfg, hw, numWarps, ringBytes, db) : ringBytes;
     const double ctasBySmem = std::floor(hw.smemBytesPerSM / smemBytesPerCta);
-    const double ctasByWarps = std::floor(double(hw.maxWarpsPerSM) / numWarps);
-    const double ctasByRegs = workgroupsByRegisters(cfg, hw, numWarps, threadsPerCta);
+    const double ctasByWarps = std::floor(double(hw.maxWarpsPerSM) / residentWarps);
+    const double ctasByRegs = workgroupsByRegisters(cfg, hw, residentWarps, threadsPerCta);
     const double ctasPerSM =
         std::min(std::min(ctasBySmem, ctasByWarps), std::min(ctasByRegs, double(hw.maxCtasPerSM)));
     if (ctasPerSM < 1.0) {
@@ -173,7 +199,16 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const double tPrologue = prologueTiles * tileBytes / gmemBytesPerCycle / ctasPerSM;
     const double tEpilogue = double(cfg.BM) * cfg.BN * double(hw.cBytes) / gmemBytesPerCycle / ctasPerSM;
     const double tBody = kSteps * tStep;
-    const double envelopeEfficiency = tBody / (tPrologue + tBody + tEpilogue);
+    double envelopeEfficiency;
+    if (persistent) {
+        // One workgroup per slot walks the busiest slot's ceil(tiles / slots)
+        // tiles: one fill, that many bodies (each tile's stores drain under the
+        // next body), one drain.
+        const double walked = tBody * fullWaves;
+        envelopeEfficiency = walked / (tPrologue + walked + tEpilogue);
+    } else {
+        envelopeEfficiency = tBody / (tPrologue + tBody + tEpilogue);
+    }
     p.kSteps = kSteps;
     p.tPrologueCycles = tPrologue;
     p.tEpilogueCycles = tEpilogue;

@@ -35,6 +35,7 @@ GemmConfig toCpp(const ridge_model_config_t& c) {
     g.stages = c.stages;
     g.regsPerThread = c.regsPerThread;
     g.groupM = c.groupM;
+    g.schedule = c.schedule;
     return g;
 }
 
@@ -59,6 +60,7 @@ void ridge_model_default_config(ridge_model_config_t* cfg) {
     cfg->stages = g.stages;
     cfg->regsPerThread = g.regsPerThread;
     cfg->groupM = g.groupM;
+    cfg->schedule = g.schedule;
 }
 
 void* ridge_model_hw_load(const char* spec, char* err, size_t errcap) {

@@ -38,6 +38,23 @@ namespace ridgeh {
         }                                                                                           \
     } while (0)
 
+// MI355X in its whole-device mode: 256 CUs, gfx950. A compute-partitioned GPU
+// (CPX, DPX, ...) exposes a fraction of the CUs and XCDs as a device of its own;
+// its throughput, wave quantisation and L2 layout are not the ones the sweep
+// and the calibration describe, so the harnesses refuse it the way the
+// reference's setup refuses a MIG slice (setup-box.sh:37-41) unless told
+// otherwise.
+constexpr int kWholeDeviceCus = 256;
+
+inline void requireWholeDevice(const hipDeviceProp_t& prop, bool allowPartitioned) {
+    const bool gfx950 = std::string(prop.gcnArchName).rfind("gfx950", 0) == 0;
+    if (gfx950 && prop.multiProcessorCount == kWholeDeviceCus) return;
+    std::fprintf(stderr, "device %s (%s) with %d CUs is not a whole MI355X (gfx950, %d CUs)%s\n", prop.name,
+                 prop.gcnArchName, prop.multiProcessorCount, kWholeDeviceCus,
+                 allowPartitioned ? "; continuing (--allow-partitioned)" : "; pass --allow-partitioned to run anyway");
+    if (!allowPartitioned) std::exit(3);
+}
+
 inline double seconds() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }

@@ -8,7 +8,8 @@
 // a drift above 5% fails the run; a variant that cannot be measured is a failure,
 // not a silent skip.
 //
-//   ridge-measure [sweep.csv] [out.csv] [--allow-skip] [--warmup-seconds S] [--settle-seconds T]
+//   ridge-measure [sweep.csv] [out.csv] [--allow-skip] [--allow-partitioned] [--warmup-seconds S]
+//                 [--settle-seconds T]
 //
 // --settle-seconds (default 0.2): every timed measurement -- each variant, each
 // hipBLASLt comparator and each canary -- first runs its own workload untimed for
@@ -22,9 +23,10 @@
 // instead of failing (for shapes such as N = 128 that only some tiles divide).
 //
 // Columns: M,N,K,tag,BM,BN,BK,WM,WN,stages,groupM,regsPerThread,smemBytes,threads,
-// tflops,blas_tflops,fraction_of_blas,canary_tflops,ms,iters -- the reference's
-// columns (measure.cu:227-234, with its cuBLAS pair now hipBLASLt) plus the
-// per-launch time and iteration count.
+// tflops,blas_tflops,fraction_of_blas,canary_tflops,ms,iters,schedule -- the
+// reference's columns (measure.cu:227-234, with its cuBLAS pair now hipBLASLt)
+// plus the per-launch time, the iteration count and the row's schedule
+// (0 uniform, 1 ping-pong, 2 persistent; ridge_gemm_variant_t.schedule).
 
 #include "harness.hpp"
 
@@ -86,11 +88,13 @@ std::vector<Shape> loadRegisteredSweep(const char* path) {
 int main(int argc, char** argv) {
     std::vector<std::string> pos;
     bool allowSkip = false;
+    bool allowPartitioned = false;
     double warmSeconds = 5.0;
     double settleSeconds = 0.2;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if (a == "--allow-skip") allowSkip = true;
+        else if (a == "--allow-partitioned") allowPartitioned = true;
         else if (a == "--warmup-seconds" && i + 1 < argc) warmSeconds = std::atof(argv[++i]);
         else if (a == "--settle-seconds" && i + 1 < argc) settleSeconds = std::atof(argv[++i]);
         else pos.push_back(a);
@@ -102,8 +106,7 @@ int main(int argc, char** argv) {
     RIDGE_HIP_CHECK(hipGetDeviceProperties(&prop, 0));
     std::printf("GPU: %s (%s), %d CUs, clock %.0f MHz\n", prop.name, prop.gcnArchName, prop.multiProcessorCount,
                 prop.clockRate / 1000.0);
-    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
-        std::printf("WARNING: this sweep targets gfx950.\n");
+    requireWholeDevice(prop, allowPartitioned);
 
     const std::vector<Shape> shapes = loadRegisteredSweep(sweepPath.c_str());
     const int nv = ridge_gemm_num_variants();
@@ -166,7 +169,7 @@ int main(int argc, char** argv) {
         << "# settle_seconds," << settleSeconds << "\n"
         << "# canary_start_tflops," << canaryFirst << "\n"
         << "M,N,K,tag,BM,BN,BK,WM,WN,stages,groupM,regsPerThread,smemBytes,threads,"
-           "tflops,blas_tflops,fraction_of_blas,canary_tflops,ms,iters\n";
+           "tflops,blas_tflops,fraction_of_blas,canary_tflops,ms,iters,schedule\n";
     out.flush();
 
     int measurements = 0, skipped = 0, failed = 0;
@@ -203,7 +206,8 @@ int main(int argc, char** argv) {
             out << s.M << ',' << s.N << ',' << s.K << ',' << s.tag << ',' << kv.BM << ',' << kv.BN << ',' << kv.BK
                 << ',' << kv.WM << ',' << kv.WN << ',' << kv.stages << ',' << kv.groupM << ',' << kv.regsPerThread
                 << ',' << kv.ldsBytes << ',' << kv.threads << ',' << t.tflops << ',' << blasTflops << ','
-                << (t.tflops / blasTflops) << ',' << canaryNow << ',' << t.ms << ',' << t.iters << '\n';
+                << (t.tflops / blasTflops) << ',' << canaryNow << ',' << t.ms << ',' << t.iters << ','
+                << kv.schedule << '\n';
             out.flush();
             std::printf("    %2d %3dx%3dx%2d w%3dx%3d s%d g%-2d  %8.2f TFLOP/s  %5.1f%% of hipBLASLt\n", v, kv.BM,
                         kv.BN, kv.BK, kv.WM, kv.WN, kv.stages, kv.groupM, t.tflops, 100.0 * t.tflops / blasTflops);

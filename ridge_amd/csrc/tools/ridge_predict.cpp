@@ -5,10 +5,12 @@
 //
 //   ridge-predict [--gpu a100|mi355x | --hw model.json] [--m M --n N --k K]
 //                 [--bm BM --bn BN --bk BK --warpm WM --warpn WN --stages S --regs R]
+//                 [--groupm G --schedule S]
 //                 [--batch in.csv --out out.csv]
 //
 // Batch mode: lines starting with '#' pass through; the first other line is the
-// header; columns are matched by name (M,N,K,BM,BN,BK,WM,WN,stages,regsPerThread),
+// header; columns are matched by name (M,N,K,BM,BN,BK,WM,WN,stages,regsPerThread,
+// and this build's groupM and schedule),
 // missing ones take GemmConfig defaults, extra ones pass through; each row gets
 // pred_tflops,pred_bottleneck,pred_compute_ceiling,pred_hbm_ceiling,pred_smem_eff,
 // pred_occ_factor,pred_arith_intensity,pred_ctas_per_sm appended, written with the
@@ -37,6 +39,7 @@ void usage() {
         "                [--m M --n N --k K]\n"
         "                [--bm BM --bn BN --bk BK --warpm WM --warpn WN]\n"
         "                [--stages S --regs R]\n"
+        "                [--groupm G --schedule -1|0|1|2]  (uniform, ping-pong, persistent)\n"
         "                [--batch in.csv --out out.csv]\n"
         "Defaults: A100 placeholders, 4096^3, 128x128x32 tile, 64x64 warp tile, 3 stages.\n");
 }
@@ -96,6 +99,7 @@ int runBatch(const std::string& inPath, const std::string& outPath, const Hardwa
         cfg.stages = int(col("stages", cfg.stages));
         cfg.regsPerThread = int(col("regsPerThread", cfg.regsPerThread));
         cfg.groupM = int(col("groupM", cfg.groupM));
+        cfg.schedule = int(col("schedule", cfg.schedule));
         const Prediction p = predict(cfg, hw);
         out << line << ',' << p.predictedTFLOPS << ',' << toString(p.bottleneck) << ',' << p.computeTFLOPS << ','
             << p.hbmTFLOPS << ',' << p.smEfficiency << ',' << p.occFactor << ',' << p.arithmeticIntensity << ','
@@ -130,6 +134,8 @@ int main(int argc, char** argv) {
         else if (a == "--warpn") cfg.warpN = int(next(cfg.warpN));
         else if (a == "--stages") cfg.stages = int(next(cfg.stages));
         else if (a == "--regs") cfg.regsPerThread = int(next(cfg.regsPerThread));
+        else if (a == "--groupm") cfg.groupM = int(next(cfg.groupM));
+        else if (a == "--schedule") cfg.schedule = int(next(cfg.schedule));
         else if (a == "-h" || a == "--help") {
             usage();
             return 0;

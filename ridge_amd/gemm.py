@@ -37,7 +37,9 @@ class RidgeGemmError(RuntimeError):
 class _VariantStruct(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "BM", "BN", "BK", "WM", "WN", "stages", "groupM", "ldsBytes", "threads", "regsPerThread",
-        "waves", "vgprs", "agprs", "sgprs", "scratchBytes", "occupancy", "pingPong")]
+        "waves", "vgprs", "agprs", "sgprs", "scratchBytes", "occupancy", "pingPong", "schedule")]
+
+SCHEDULES = {0: "uniform", 1: "ping-pong", 2: "persistent"}
 
 
 @dataclass(frozen=True)
@@ -60,6 +62,7 @@ class Variant:
     scratchBytes: int
     occupancy: int
     pingPong: int
+    schedule: int
 
     @property
     def smemBytes(self):
@@ -72,8 +75,14 @@ class Variant:
     def key(self):
         return (self.BM, self.BN, self.BK, self.WM, self.WN, self.stages, self.groupM)
 
+    @property
+    def schedule_name(self):
+        return SCHEDULES.get(self.schedule, "unknown")
+
     def label(self):
-        return "%dx%dx%d w%dx%d s%d g%d" % self.key()
+        """BMxBNxBK wWMxWN sS gG, with " persistent" for the store-behind rows."""
+        base = "%dx%dx%d w%dx%d s%d g%d" % self.key()
+        return base + " persistent" if self.schedule == 2 else base
 
     def as_dict(self):
         return asdict(self)

@@ -37,8 +37,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # data/hardware/mi355x.json at registration time): selection and scoring use it,
 # so a later re-calibration cannot change the registered configs or thresholds.
 HW_JSON = os.path.join(ROOT, "data", "sweep", "rocprof-label-hw.json")
-SOURCES = [os.path.join(ROOT, "data", "measured", "mi355x.csv"),
-           os.path.join(ROOT, "data", "measured", "mi355x-baseline-configs.csv")]
+# The measured rows the selection was made from (frozen copies of
+# data/measured/mi355x.csv and mi355x-baseline-configs.csv at registration
+# time), for the same reason: re-measuring the sweep after a kernel change must
+# not change the registered configs.
+SOURCES = [os.path.join(ROOT, "data", "sweep", "rocprof-label-sweep.csv"),
+           os.path.join(ROOT, "data", "sweep", "rocprof-label-baseline-configs.csv")]
 CONFIGS_CSV = os.path.join(ROOT, "data", "sweep", "rocprof-label-configs.csv")
 COUNTERS_CSV = os.path.join(ROOT, "data", "measured", "rocprof-labels.csv")
 
@@ -63,7 +67,7 @@ PASS1_COUNTERS = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_WAVE_CYCL
                   "SQ_WAVES", "SQ_INSTS_MFMA", "GRBM_GUI_ACTIVE", "GRBM_COUNT"]
 
 KEY_FIELDS = ["BM", "BN", "BK", "WM", "WN", "stages", "groupM"]
-# 4096^3 with the bench's default variant.
+# 4096^3 with the bench's default variant at registration time.
 CONTROL = (4096, 4096, 4096, 256, 256, 32, 128, 64, 4, 4)
 CONTROL_SIMD_UTIL_PCT = (80.0, 105.0)
 
@@ -158,7 +162,9 @@ def cmd_run(args):
     for i, c in enumerate(configs):
         idx = G.find_variant(*[c[k] for k in KEY_FIELDS])
         if idx < 0:
-            raise SystemExit("config %d: variant not in the kernel table" % i)
+            raise SystemExit("config %d: variant not in the kernel table (a row retired after the "
+                             "registration; its counters were gathered and scored before, and a replay "
+                             "needs the table of the registration commit)" % i)
         if not G.variant(idx).divides(c["M"], c["N"], c["K"]):
             raise SystemExit("config %d: variant does not divide the shape" % i)
         M, N, K = c["M"], c["N"], c["K"]

@@ -22,7 +22,7 @@ BOTTLENECKS = ["TENSOR_CORE", "SMEM", "HBM", "OCC", "WAVES", "ENVELOPE", "DOES_N
 class _Config(ctypes.Structure):
     _fields_ = [("M", ctypes.c_longlong), ("N", ctypes.c_longlong), ("K", ctypes.c_longlong)] + \
                [(n, ctypes.c_int) for n in ("BM", "BN", "BK", "warpM", "warpN", "mmaM", "mmaN", "mmaK",
-                                           "stages", "regsPerThread", "groupM")]
+                                           "stages", "regsPerThread", "groupM", "schedule")]
 
 
 _PRED_FIELDS = [("predictedTFLOPS", ctypes.c_double), ("bottleneck", ctypes.c_int)] + \

@@ -42,10 +42,23 @@ def test_table_has_24_registered_rows_with_consistent_fields():
     assert len(set(keys)) == 24
     for v in vs:
         assert v.BM in (64, 128, 256) and v.BN in (64, 128, 256) and v.BK in (32, 64)
-        assert 2 <= v.stages <= 5
-        assert v.waves == (v.BM // v.WM) * (v.BN // v.WN)
+        compute_waves = (v.BM // v.WM) * (v.BN // v.WN)
+        ring = v.stages * (v.BM * v.BK + v.BK * v.BN) * 2
+        assert v.schedule in (0, 1, 2)
+        assert v.pingPong == (1 if v.schedule == 1 else 0)
+        if v.schedule == 2:
+            # Persistent: two loader wavefronts; LDS = ring + a 16-row-multiple
+            # staging region per compute wavefront.
+            assert 2 <= v.stages <= 8
+            assert v.waves == compute_waves + 2
+            staging = v.ldsBytes - ring
+            assert staging > 0 and staging % (compute_waves * 16 * v.WN * 2) == 0
+        else:
+            assert 2 <= v.stages <= 5
+            assert v.waves == compute_waves
+            assert v.ldsBytes == ring
+            assert v.schedule == (1 if v.waves == 8 and v.stages >= 3 else 0)
         assert v.threads == 64 * v.waves
-        assert v.ldsBytes == v.stages * (v.BM * v.BK + v.BK * v.BN) * 2
         assert v.ldsBytes <= 160 * 1024
         assert v.regsPerThread == v.vgprs + v.agprs and v.regsPerThread > 0
         assert v.occupancy >= 1
@@ -81,7 +94,17 @@ def test_variant_table_csv():
     lines = text.strip().splitlines()
     assert lines[0].startswith("idx,BM,BN,BK,WM,WN,stages,groupM,ldsBytes,threads,regsPerThread")
     assert len(lines) == 25
-    row = lines[1].split(",")
-    v = G.variant(0)
-    assert [int(x) for x in row[:11]] == [0, v.BM, v.BN, v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes,
-                                          v.threads, v.regsPerThread]
+    assert lines[0].endswith(",pingPong,schedule")
+    for i in (0, len(lines) - 2):
+        row = lines[i + 1].split(",")
+        v = G.variant(i)
+        assert [int(x) for x in row[:11]] == [i, v.BM, v.BN, v.BK, v.WM, v.WN, v.stages, v.groupM, v.ldsBytes,
+                                              v.threads, v.regsPerThread]
+        assert int(row[-1]) == v.schedule
+    assert sum(1 for l in lines[1:] if l.endswith(",2")) == sum(1 for v in G.variants() if v.schedule == 2) >= 1
+
+
+def test_persistent_rows_are_labelled():
+    ps = [v for v in G.variants() if v.schedule == 2]
+    assert ps and all(v.label().endswith(" persistent") and v.schedule_name == "persistent" for v in ps)
+    assert all(not v.label().endswith("persistent") for v in G.variants() if v.schedule != 2)

@@ -312,3 +312,62 @@ def test_hardware_json_loader_is_all_or_nothing(tmp_path):
         RM.Hardware(str(zero))
     with pytest.raises(ValueError, match="cannot open"):
         RM.Hardware(str(tmp_path / "missing.json"))
+
+
+def test_mi355x_persistent_rows_walk_tiles_and_pay_one_fill_and_drain(mi355x):
+    """8192 x 8192 x 128, 128x128x64 tile, 64x64 wavefront tile, 4 stages, 185
+    registers, schedule 2 (persistent store-behind) on the MI355X placeholders.
+
+      compute waves  (128/64) x (128/64) = 4, plus 2 loader waves = 6
+      MFMA/wave/step (64/16) x (64/16) x (64/32) = 32 -> tCompute 32 x 4 x 4 = 512
+      tSmem          4 x (64 + 64) x 64 x 2 B = 65536 B / 128 = 512
+      tStep          512 + 512 = 1024 (no ping-pong), smEff 0.5
+      LDS            ring 4 x (128x64 + 64x128) x 2 = 131072, staging 4 waves x 16
+                     rows x 4 tile-rows x 64 x 2 B = 32768 -> 163840 -> 1 per CU
+      registers      185 -> 192; floor(512/192) = 2 waves/SIMD; 6 waves over 4
+                     SIMDs = 2 per SIMD -> 1 workgroup
+      latency        4 compute waves x 1 / 8 needed = 0.5 (placeholders measure no
+                     ILP-8 column)
+      grid           64 x 64 = 4096 tiles over 256 slots = 16 tiles per slot
+      prologue       min(3, 128/64) = 2 tiles x 32768 B / 13.0208333 = 5033.1648
+      epilogue       128 x 128 x 2 / 13.0208333 = 2516.5824
+      envelope       16 x 2048 / (5033.1648 + 16 x 2048 + 2516.5824) = 0.812744
+                     (schedule -1, one tile per workgroup: 2048 / 9597.7472 = 0.213383)
+      compute        2516.5824 x 0.5 x 0.5 x 1 x 0.812744 = 511.334
+      HBM            compulsory 2 x 8192^2 x 128 / ((2 x 8192 x 128 + 8192^2) x 2)
+                     = 124.1212 FLOP/B -> 8e12 x 124.1212 = 992.97 TFLOP/s
+    """
+    cfg = dict(M=8192, N=8192, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=4, regsPerThread=185,
+               groupM=8)
+    p = RM.predict(mi355x, schedule=2, **cfg)
+    assert p["numWarps"] == 4 and p["ctasPerSM"] == 1
+    assert p["tStepCycles"] == pytest.approx(1024.0) and p["smEfficiency"] == pytest.approx(0.5)
+    assert p["occFactor"] == pytest.approx(0.5)
+    assert p["wavesExact"] == pytest.approx(16.0) and p["waveEfficiency"] == pytest.approx(1.0)
+    assert p["tPrologueCycles"] == pytest.approx(5033.1648, abs=1e-3)
+    assert p["tEpilogueCycles"] == pytest.approx(2516.5824, abs=1e-3)
+    assert p["envelopeEfficiency"] == pytest.approx(32768 / 40317.7472, abs=1e-9)
+    assert p["computeTFLOPS"] == pytest.approx(2516.5824 * 0.25 * 32768 / 40317.7472, abs=1e-6)
+    assert p["compulsoryIntensity"] == pytest.approx(17179869184 / 138412032, abs=1e-9)
+    assert p["hbmTFLOPS"] == pytest.approx(8 * 17179869184 / 138412032, abs=1e-6)
+    assert p["predictedTFLOPS"] == pytest.approx(p["computeTFLOPS"])
+    one = RM.predict(mi355x, schedule=-1, **cfg)
+    assert one["envelopeEfficiency"] == pytest.approx(2048 / 9597.7472, abs=1e-9)
+    # An explicit uniform schedule is the derived one for a 4-wave row.
+    assert RM.predict(mi355x, schedule=0, **cfg) == one
+
+
+def test_mi355x_persistent_occupancy_counts_loaders_and_staging(mi355x):
+    """64x64x32 tile, 32x32 wavefront tiles (4 compute waves), registers unknown.
+    Persistent: 6 waves -> floor(32/6) = 5 by wave slots; LDS ring + staging:
+      s4: 4 x (64x32 + 32x64) x 2 = 32768 + 4 x 16 x 2 x 32 x 2 = 8192 -> 40960
+          -> floor(163840/40960) = 4 (the ring alone would allow 5)
+      s2: 16384 + 8192 = 24576 -> 6, so the wave slots bind: 5
+    One tile per workgroup: 4 waves -> 8 slots; s4 LDS 32768 -> 5."""
+    base = dict(M=4096, N=4096, K=4096, BM=64, BN=64, BK=32, warpM=32, warpN=32, regsPerThread=0)
+    assert RM.predict(mi355x, stages=4, schedule=2, **base)["ctasPerSM"] == 4
+    assert RM.predict(mi355x, stages=2, schedule=2, **base)["ctasPerSM"] == 5
+    assert RM.predict(mi355x, stages=4, schedule=-1, **base)["ctasPerSM"] == 5
+    # The A100 model has no persistent term: the schedule field is ignored.
+    a100 = RM.Hardware("a100")
+    assert RM.predict(a100, stages=4, schedule=2, **base) == RM.predict(a100, stages=4, schedule=-1, **base)
