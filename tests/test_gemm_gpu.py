@@ -107,9 +107,12 @@ def test_small_integer_inputs_bit_exact_every_variant(M, N, K):
         assert bad == 0, "%s: %d of %d outputs differ" % (v.label(), bad, M * N)
 
 
-def test_headline_4096_exact_integers_and_identity():
+@pytest.mark.parametrize("key", [(256, 256, 32, 128, 64, 3, 4), (256, 256, 32, 128, 64, 4, 4)])
+def test_headline_4096_exact_integers_and_identity(key):
+    """The bench's default variant (s3 g4) and its s4 neighbour at the headline shape."""
     M = N = K = 4096
-    best = G.find_variant(256, 256, 32, 128, 64, 4, 4)
+    best = G.find_variant(*key)
+    assert best >= 0
     Ab, Bb, want = _exact_case(M, N, K, -2, 2, 4096)
     A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
     got = _bits(_run(best, A, B, M, N, K))
@@ -120,6 +123,36 @@ def test_headline_4096_exact_integers_and_identity():
     G.fill_uniform(Bu, 9)
     C = _run(best, eye, Bu, M, N, K)
     assert torch.equal(C.view(torch.int16), Bu.view(torch.int16))
+
+
+def _persistent_edge_shapes(v):
+    """Shapes that drive the persistent schedule's control flow to its edges."""
+    BM, BN, BK, S = v.BM, v.BN, v.BK, v.stages
+    return [
+        (BM, BN, BK),                        # one output tile, one K tile
+        (BM, BN, BK * max(1, S - 2)),         # fewer K tiles than the ring prefetches
+        (2 * BM, 3 * BN, 5 * BK),             # six tiles: a grid far below one per CU
+        (4096, 4096, BK),                     # many tiles per workgroup, one K tile each
+        (37 * BM, 11 * BN, 3 * BK),           # 407 tiles: some workgroups walk one more
+        (2048, 1024, (2 * S + 1) * BK),       # K tiles wrap the ring more than twice
+    ]
+
+
+def test_persistent_rows_edge_shapes_bit_exact():
+    """Every persistent (store-behind) row on its edge shapes, small-integer
+    inputs: the FP16 output equals the exact product rounded once, and no output
+    is left unwritten (C starts as NaN, which would not compare equal)."""
+    rows = [v for v in G.variants() if v.schedule == 2]
+    assert rows
+    for v in rows:
+        for (M, N, K) in _persistent_edge_shapes(v):
+            assert v.divides(M, N, K), (v.label(), M, N, K)
+            print("  %s %dx%dx%d" % (v.label(), M, N, K), flush=True)
+            Ab, Bb, want = _exact_case(M, N, K, -3, 3, M + 7 * N + 13 * K)
+            A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+            got = _bits(_run(v.index, A, B, M, N, K))
+            bad = int(np.count_nonzero(got != want))
+            assert bad == 0, "%s on %dx%dx%d: %d of %d outputs differ" % (v.label(), M, N, K, bad, M * N)
 
 
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 128),
