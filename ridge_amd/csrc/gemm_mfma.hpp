@@ -639,10 +639,10 @@ void gemmMfmaPingPongKernel(const _Float16* __restrict__ A, const _Float16* __re
 // ---------------------------------------------------------------------------
 // Persistent store-behind schedule, for shapes whose cost is writing C (small K).
 //
-// One workgroup per CU walks the output tiles r, r + grid, r + 2 grid, ... of
-// its logical id r (XCD remap, then GroupM order, as above), so at round j each
-// XCD works on a compact block of 32 tiles. The workgroup has two kinds of
-// wavefronts:
+// One workgroup per CU slot walks the output tiles r, r + grid, r + 2 grid, ...
+// of its logical id r (XCD remap, then GroupM order, as above), so at round j
+// each XCD works on a compact block of grid / 8 tiles (32 on a 256-CU grid). The
+// workgroup has two kinds of wavefronts:
 //  * compute waves 0 .. kWaves-1 (the tile's wave grid) read fragments, run the
 //    MFMAs and, after a tile's last K tile, convert and store it through a
 //    private LDS staging region (storeStaged). They issue no global loads, so
