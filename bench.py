@@ -82,21 +82,41 @@ def time_launches(fn, steps, stream):
     return wall, e0.elapsed_time(e1)
 
 
+def calibrated_peaks():
+    """The calibrated chip's own ceilings (data/hardware/mi355x.json): the MFMA
+    rate a pure matrix load sustains at its loaded clock, and the HBM copy rate."""
+    try:
+        with open(HARDWARE_JSON) as f:
+            hw = json.load(f)
+        return float(hw["impliedPeakTflops"]), float(hw["hbmBytesPerSec"]) / 1e9
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def roofline(M, N, K, per_launch_ms, traffic):
     """The bound the shape's arithmetic intensity puts it under (datasheet ridge
     point 2516.6 / 8 = 315 FLOP/B) and the algorithmic rate against it: FLOP/s for
     MFMA-bound shapes, compulsory bytes 2(MK + KN + MN) per second for HBM-bound
-    ones, from the HIP-event time per launch."""
+    ones, from the HIP-event time per launch. `peak` and `frac` are against the
+    datasheet; `calibrated_peak` and `calibrated_frac` against the calibration."""
     flops = 2.0 * M * N * K
     nbytes = 2.0 * (M * K + K * N + M * N)
     sec = per_launch_ms * 1e-3
+    cal_mfma, cal_hbm = calibrated_peaks()
     if flops / nbytes >= PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
         achieved = flops / sec / 1e12
-        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic}
-    achieved = nbytes / sec / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic}
+        out = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic}
+        cal = cal_mfma
+    else:
+        achieved = nbytes / sec / 1e9
+        out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+               "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic}
+        cal = cal_hbm
+    if cal:
+        out["calibrated_peak"] = round(cal, 1)
+        out["calibrated_frac"] = round(achieved / cal, 4)
+    return out
 
 
 # Infinity Cache (MALL) of MI355X: 256 MB, shared by all XCDs in front of HBM.
