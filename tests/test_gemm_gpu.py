@@ -134,6 +134,7 @@ def _persistent_edge_shapes(v):
         (2 * BM, 3 * BN, 5 * BK),             # six tiles: a grid far below one per CU
         (4096, 4096, BK),                     # many tiles per workgroup, one K tile each
         (37 * BM, 11 * BN, 3 * BK),           # 407 tiles: some workgroups walk one more
+        (800 * BM, 3 * BN, 2 * BK),           # 2400 tiles: 9-10 per workgroup
         (2048, 1024, (2 * S + 1) * BK),       # K tiles wrap the ring more than twice
     ]
 
