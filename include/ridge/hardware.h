@@ -58,6 +58,16 @@ struct HardwareModel {
                                      //    the epilogue staging join the workgroup, which walks
                                      //    ceil(tiles / slots) tiles and pays one fill and one
                                      //    drain for all of them
+    int ldsReadModel = 0;            // 0: one blended operand-read rate, smemBytesPerCycle (reference)
+                                     // 1: A fragments at ldsAReadBytesPerCycle (ds_read_b128),
+                                     //    B fragments at ldsBTrReadBytesPerCycle (transposing reads)
+    double ldsAReadBytesPerCycle = 0.0;    // [CAL] per CU, read by ldsReadModel 1
+    double ldsBTrReadBytesPerCycle = 0.0;  // [CAL] per CU, read by ldsReadModel 1
+    int clockModel = 0;              // 0: every wave of workgroups runs at clockHz (reference)
+                                     // 1: the chip is power-limited: a last wave that leaves CUs
+                                     //    idle runs at clockHz x clockRatio for its busy share
+    double clockRatio[4] = {0.0, 0.0, 0.0, 0.0};  // [CAL] loaded clock with 1/2, 1/4, 1/8, 1/16 of the
+                                                  // CUs busy, over the clock with all of them busy
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -48,6 +48,9 @@ struct Prediction {
     double reuseTilesM = 0.0;          // resident row tiles sharing one XCD's L2
     double reuseTilesN = 0.0;          // resident column tiles sharing it
     double compulsoryIntensity = 0.0;  // 2MNK / (A + B + C bytes)
+
+    // Power-limited clock (clockModel 1; 1.0 otherwise).
+    double tailClockFactor = 1.0;      // clock of the last wave over the full-chip clock
 };
 
 }  // namespace ridge

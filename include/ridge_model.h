@@ -41,6 +41,7 @@ typedef struct ridge_model_prediction {
     int numWarps, ctasPerSM;
     double tComputeCycles, tSmemCycles, tStepCycles;
     double reuseTilesM, reuseTilesN, compulsoryIntensity;
+    double tailClockFactor;  /* clock of the last wave over the full-chip clock (clockModel 1) */
 } ridge_model_prediction_t;
 
 /* Default config (the reference's GemmConfig defaults, config.h:18-39). */

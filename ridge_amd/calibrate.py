@@ -17,7 +17,12 @@ MI355X differences from the reference driver:
   * the compute band is checked on the peak implied at the nominal clock (what
     the cycle count alone says), the loaded-clock figure is reported beside it;
   * the JSON carries the CDNA4 target description ("arch": "gfx950") and the
-    extra measured keys (MALL bandwidth, LDS control and per-pattern rates).
+    extra measured keys (MALL bandwidth, LDS control and per-pattern rates);
+  * the chip is power-limited, so cal-mma also measures the loaded clock with
+    1/2 .. 1/16 of the CUs busy (clockRatio*: the model's clockModel 1), and the
+    per-operand LDS rates feed ldsReadModel 1;
+  * cal-smem-bw's ping-pong skeleton figures (reads under MFMAs, with and without
+    the GEMM's direct-to-LDS refill) are kept in the JSON as a record.
 """
 
 import argparse
@@ -93,11 +98,29 @@ def band_check(res, spec):
     ok &= check("hbmBytesPerSec", res["hbmBytesPerSec"] / 1e12, spec["hbm_bytes_per_sec"] * 0.60 / 1e12,
                 spec["hbm_bytes_per_sec"] * 1.02 / 1e12, "TB/s", "above spec would mean the MALL, not HBM")
     ok &= check("warpsNeededToHide", res["warpsNeededToHide"], 1, 32, "waves/CU")
+    # A partly busy chip clocks at least as fast as a full one (within noise) and
+    # never past the engine clock's ceiling.
+    ceiling = spec["clock_hz"] * 1.05 / res["clockHz"]
+    for key in CLOCK_RATIO_KEYS:
+        ok &= check(key, res[key], 0.98, ceiling, "x", "over the full-chip loaded clock")
+    ok &= check("ldsAReadBytesPerCycle", res["ldsAReadBytesPerCycle"], 0.25 * res["ldsControlBytesPerCycle"],
+                1.05 * res["ldsControlBytesPerCycle"], "B/cycle/CU")
+    ok &= check("ldsBTrReadBytesPerCycle", res["ldsBTrReadBytesPerCycle"], 0.125 * res["ldsControlBytesPerCycle"],
+                1.05 * res["ldsControlBytesPerCycle"], "B/cycle/CU")
     return ok
 
 
+CLOCK_RATIO_KEYS = ["clockRatioHalfCus", "clockRatioQuarterCus", "clockRatioEighthCus", "clockRatioSixteenthCus"]
+
+# Figures of the ping-pong skeleton (cal-smem-bw), kept in the JSON as a record;
+# the model reads none of them.
+SKELETON_KEYS = ["pingPongStepCycles", "pingPongReadCycles", "pingPongMfmaCycles", "pingPongRefillStepCycles",
+                 "pingPongStepCyclesClockHz", "pingPongMfmaCyclesClockHz", "pingPongRefillStepCyclesClockHz",
+                 "phaseSwitchCycles"]
+
+
 def hardware_json(res, spec, arch):
-    return {
+    out = {
         "name": spec["name"],
         "arch": arch,
         "note": ("measured by ridge_amd/calibrate.py on a %s; clockHz is the loaded clock measured by cal-mma "
@@ -134,7 +157,15 @@ def hardware_json(res, spec, arch):
         "ldsBTrReadBytesPerCycle": res.get("ldsBTrReadBytesPerCycle", 0.0),
         "mfma32x32x16CyclesPerInst": res.get("mfma32x32x16CyclesPerInst", 0.0),
         "mfma32x32x16ClockHz": res.get("mfma32x32x16ClockHz", 0.0),
+        "ldsReadModel": 1,
+        "clockModel": 1,
     }
+    for key in CLOCK_RATIO_KEYS:
+        out[key] = res[key]
+    for key in SKELETON_KEYS:
+        if key in res:
+            out[key] = res[key]
+    return out
 
 
 def main(argv=None):
@@ -172,7 +203,8 @@ def main(argv=None):
         sys.exit("no datasheet entry for %s: add one to SPECS rather than reusing another card's" % arch)
     spec = SPECS[arch]
     required = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
-                "smemBytesPerCycle", "ldsControlBytesPerCycle", "hbmBytesPerSec", "warpsNeededToHide"]
+                "smemBytesPerCycle", "ldsControlBytesPerCycle", "ldsAReadBytesPerCycle", "ldsBTrReadBytesPerCycle",
+                "hbmBytesPerSec", "warpsNeededToHide"] + CLOCK_RATIO_KEYS
     missing = [k for k in required if k not in results]
     if missing:
         sys.exit("benchmarks did not report: %s" % ", ".join(missing))

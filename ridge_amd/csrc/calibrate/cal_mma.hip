@@ -117,7 +117,9 @@ __global__ __launch_bounds__(Waves * 64) void mfmaThroughputKernel(const half8_t
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
 }
 
-// Median cycles per MFMA on one CU (Waves waves issuing) and the loaded clock.
+// Median cycles per MFMA on one CU (Waves waves issuing) and the loaded clock,
+// over `cus` workgroups (one per CU; fewer than the chip's CUs leaves the rest
+// idle).
 template <int Waves, int Shape>
 void measure(int cus, const half8_t* dOperands, float* dSink, Stamp* dStamps, double& cyclesPerMfma,
              double& clockHz) {
@@ -210,6 +212,36 @@ int main() {
     std::printf("CAL_INFO mfma32x32x16CyclesPerInst %.6f\n", c32);
     std::printf("CAL_INFO mfma32x32x16ClockHz %.6e\n", hz32);
 
+    // The loaded clock against the share of CUs kept busy. The chip is power-
+    // limited under a full matrix load; a launch that fills only part of it (the
+    // last wave of a grid that does not divide the CU count) runs faster per CU.
+    // Same saturated stream (4 waves per CU) on cus / d workgroups.
+    std::printf("\nloaded clock against busy CUs (4 waves per CU, same operands)\n  %8s %14s\n", "CUs", "clock MHz");
+    const int kFractions[] = {2, 4, 8, 16};
+    double clockAt[5] = {0, 0, 0, 0, 0};
+    {
+        std::vector<double> clocks;
+        for (int r = 0; r < kRepeats; ++r) {
+            double c = 0, hz = 0;
+            measure<4, 0>(cus, dOperands, dSink, dStamps, c, hz);
+            clocks.push_back(hz);
+        }
+        clockAt[0] = median(clocks);
+        std::printf("  %8d %14.1f\n", cus, clockAt[0] / 1e6);
+    }
+    for (int i = 0; i < 4; ++i) {
+        const int n = cus / kFractions[i];
+        std::vector<double> clocks;
+        for (int r = 0; r < kRepeats; ++r) {
+            double c = 0, hz = 0;
+            measure<4, 0>(n, dOperands, dSink, dStamps, c, hz);
+            clocks.push_back(hz);
+        }
+        clockAt[i + 1] = median(clocks);
+        std::printf("  %8d %14.1f\n", n, clockAt[i + 1] / 1e6);
+        std::printf("CAL_CURVE busyFraction %.6f clockHz %.6e\n", 1.0 / kFractions[i], clockAt[i + 1]);
+    }
+
     const double peak = kMfmaFlops / best * bestClock * cus / 1e12;
     const double peakNominal = kMfmaFlops / best * (prop.clockRate * 1e3) * cus / 1e12;
     std::printf("\nsaturated at %d waves per CU\n", bestWaves);
@@ -224,6 +256,12 @@ int main() {
     std::printf("CAL_RESULT saturationWaves %d\n", bestWaves);
     std::printf("CAL_RESULT clockHz %.6e\n", bestClock);
     std::printf("CAL_RESULT nominalClockHz %.6e\n", prop.clockRate * 1e3);
+    // Ratios to the full-chip clock of the same sweep, so the model scales its own
+    // clockHz by them.
+    std::printf("CAL_RESULT clockRatioHalfCus %.6f\n", clockAt[1] / clockAt[0]);
+    std::printf("CAL_RESULT clockRatioQuarterCus %.6f\n", clockAt[2] / clockAt[0]);
+    std::printf("CAL_RESULT clockRatioEighthCus %.6f\n", clockAt[3] / clockAt[0]);
+    std::printf("CAL_RESULT clockRatioSixteenthCus %.6f\n", clockAt[4] / clockAt[0]);
     CAL_HIP_CHECK(hipFree(dSink));
     CAL_HIP_CHECK(hipFree(dStamps));
     CAL_HIP_CHECK(hipFree(dOperands));

@@ -83,6 +83,150 @@ __global__ __launch_bounds__(Waves * 64) void ldsReadKernel(int iters, uint32_t*
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
 }
 
+// The ping-pong schedule's skeleton: eight waves, waves w and w + 4 on SIMD w % 4,
+// group g = w / 4. A K-step has two phases separated by workgroup barriers; in
+// each, one group issues the 32 MFMAs of a 128x64 wavefront tile at BK = 32 (8 A
+// x 4 B fragments) while the other group reads the next step's fragments from the
+// swizzled tiles (8 ds_read_b128 + 8 ds_read_b64_tr_b16: 12 KiB per wave) and
+// waits for them. Modes:
+//   0  that schedule
+//   1  the reads alone (all eight waves, no barriers): checks the per-operand
+//      LDS rates against tS = A bytes / ldsAReadBytesPerCycle + B bytes /
+//      ldsBTrReadBytesPerCycle
+//   2  the MFMAs alone: tC
+//   3  mode 0 plus the GEMM's direct-to-LDS refill, 4 KiB per memory-phase wave
+//      (32 KiB per step) from a 1 MiB L2-resident buffer into a separate region
+// A perfect overlap makes mode 0 and mode 3 run at max(tC, tS) cycles; the
+// measured clock of each mode shows what the extra data movement costs in power.
+// Operands are U[-1,1) halves.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kRefillLoads = 4;              // 1 KiB direct-to-LDS loads per wave per phase
+constexpr int kRefillSourceBytes = 1 << 20;  // L2-resident source
+constexpr int kRefillRegion = 48 * 1024;     // refills land in [48 KiB, 64 KiB)
+
+template <int Mode>
+__global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, const char* refill, int iters,
+                                                      float* sink, Stamp* out) {
+    extern __shared__ __attribute__((aligned(1024))) char lds[];
+    // 48 KiB of tiles from the 16 KiB operand block, repeated.
+    for (int i = threadIdx.x; i < 48 * 1024 / 4; i += blockDim.x)
+        reinterpret_cast<uint32_t*>(lds)[i] = operands[i % (16 * 1024 / 4)];
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int group = wave / 4;
+    const uint32_t ldsBase = ridge::ldsAddress(lds);
+    int aAddr[8], bAddr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        aAddr[j] = addrA(lane, j);
+        bAddr[j] = addrB(lane, j);
+    }
+    half8_t a[8], b[4];
+    auto readFrags = [&]() {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = *(const __attribute__((address_space(3))) half8_t*)(lds + aAddr[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4_t*)(lds + bAddr[2 * j]));
+            const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4_t*)(lds + bAddr[2 * j + 1]));
+            b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+    };
+    // Load i of wave w at step it reads 1 KiB at ((it * 8 + w) * 4 + i) mod 1024
+    // KiB of the source and writes LDS [48 KiB + ((w % 4) * 4 + i) KiB, +1 KiB).
+    auto refillLoads = [&](int it) {
+#pragma unroll
+        for (int i = 0; i < kRefillLoads; ++i) {
+            const uint32_t off = (uint32_t)(((((it * 8 + wave) * kRefillLoads + i) & 1023) << 10) + lane * 16);
+            ridge::globalLoadLds16(refill, off, ldsBase + kRefillRegion + ((wave % 4) * kRefillLoads + i) * 1024);
+        }
+    };
+    float4_t acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;
+    __syncthreads();
+    readFrags();
+    constexpr bool kPingPong = Mode == 0 || Mode == 3;
+    const uint64_t c0 = cycles();
+    const uint64_t r0 = realtime();
+    if (kPingPong && group == 1) __builtin_amdgcn_s_barrier();
+    for (int it = 0; it < iters; ++it) {
+        if (Mode != 2) {
+            if (Mode == 3) refillLoads(it);
+            readFrags();
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (Mode == 3) ridge::waitVmcnt<kRefillLoads>();  // the previous phase's refill has landed
+            if (Mode == 1) {
+                // Consume every fragment register, at no instruction cost.
+#pragma unroll
+                for (int j = 0; j < 8; ++j) asm volatile("" ::"v"(a[j]));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asm volatile("" ::"v"(b[j]));
+            }
+        }
+        if (kPingPong) __builtin_amdgcn_s_barrier();
+        if (Mode != 1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc[i * 4 + j]) : "v"(a[i]), "v"(b[j]));
+        }
+        if (kPingPong) __builtin_amdgcn_s_barrier();
+    }
+    if (Mode == 3) ridge::waitVmcnt<0>();
+    if (kPingPong && group == 0) __builtin_amdgcn_s_barrier();  // both groups pass 2 * iters + 1 barriers
+    __syncthreads();
+    const uint64_t c1 = cycles();
+    const uint64_t r1 = realtime();
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) s += acc[i][0] + acc[i][3];
+    if (s == 1.2345678e30f) sink[0] = s;
+    if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
+}
+
+// Median cycles per K-step of the skeleton in `Mode` over every CU, and the
+// median loaded clock.
+template <int Mode>
+double pingPongCycles(int cus, const uint32_t* dOperands, const char* dRefill, float* dSink, Stamp* dStamps,
+                      double& clockHz) {
+    auto k = pingPongKernel<Mode>;
+    CAL_HIP_CHECK(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kOneWorkgroupLds));
+    hipLaunchKernelGGL(k, dim3(cus), dim3(512), kOneWorkgroupLds, nullptr, dOperands, dRefill, kIters, dSink,
+                       dStamps);
+    CAL_HIP_CHECK(hipGetLastError());
+    CAL_HIP_CHECK(hipDeviceSynchronize());
+    std::vector<Stamp> st(cus);
+    CAL_HIP_CHECK(hipMemcpy(st.data(), dStamps, cus * sizeof(Stamp), hipMemcpyDeviceToHost));
+    double cyc = 0.0;
+    medianStamps(st, cyc, clockHz);
+    return cyc / kIters;
+}
+
+// U[-1,1) halves from splitmix64, packed two per word: 16 KiB.
+std::vector<uint32_t> randomHalfWords() {
+    std::vector<uint32_t> w(16 * 1024 / 4);
+    uint64_t state = 0x5eedULL;
+    auto next = [&]() {
+        state += 0x9e3779b97f4a7c15ULL;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+        z ^= z >> 31;
+        const _Float16 h = (_Float16)(float(z >> 40) * (1.0f / 8388608.0f) - 1.0f);
+        return uint32_t(__builtin_bit_cast(uint16_t, h));
+    };
+    for (auto& x : w) x = next() | (next() << 16);
+    return w;
+}
+
 constexpr double bytesPerIteration(int pat) {
     // Per wave: 8 instructions of 1024 B (ds_read_b128) or 512 B (tr_b64).
     return pat == kPatB ? 8 * 512.0 : pat == kPatMix ? 4 * 1024.0 + 4 * 512.0 : 8 * 1024.0;
@@ -163,6 +307,51 @@ int main() {
         std::printf("  a pattern exceeds the conflict-free control: the benchmark is wrong\n");
         ok = false;
     }
+
+    // The ping-pong skeleton.
+    uint32_t* dOperands = nullptr;
+    char* dRefill = nullptr;
+    float* dFSink = nullptr;
+    const std::vector<uint32_t> hOperands = randomHalfWords();
+    CAL_HIP_CHECK(hipMalloc(&dOperands, hOperands.size() * sizeof(uint32_t)));
+    CAL_HIP_CHECK(hipMalloc(&dRefill, kRefillSourceBytes));
+    CAL_HIP_CHECK(hipMalloc(&dFSink, sizeof(float)));
+    CAL_HIP_CHECK(hipMemcpy(dOperands, hOperands.data(), hOperands.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    CAL_HIP_CHECK(hipMemset(dRefill, 0x3c, kRefillSourceBytes));
+    std::vector<double> st[4], hz[4];
+    for (int r = 0; r < kRepeats; ++r) {
+        double h = 0.0;
+        st[0].push_back(pingPongCycles<0>(cus, dOperands, dRefill, dFSink, dStamps, h));
+        hz[0].push_back(h);
+        st[1].push_back(pingPongCycles<1>(cus, dOperands, dRefill, dFSink, dStamps, h));
+        hz[1].push_back(h);
+        st[2].push_back(pingPongCycles<2>(cus, dOperands, dRefill, dFSink, dStamps, h));
+        hz[2].push_back(h);
+        st[3].push_back(pingPongCycles<3>(cus, dOperands, dRefill, dFSink, dStamps, h));
+        hz[3].push_back(h);
+    }
+    const char* kModeNames[4] = {"ping-pong (reads under MFMAs)", "fragment reads alone", "MFMAs alone",
+                                 "ping-pong + 32 KiB direct-to-LDS refill"};
+    const char* kModeKeys[4] = {"pingPongStepCycles", "pingPongReadCycles", "pingPongMfmaCycles",
+                                "pingPongRefillStepCycles"};
+    std::printf("\nping-pong skeleton: 8 waves (2 per SIMD), 128x64 wavefront tiles, BK = 32; per K-step per CU\n");
+    double tStep[4];
+    for (int m = 0; m < 4; ++m) {
+        tStep[m] = median(st[m]);
+        std::printf("  %-44s %8.1f cycles  %7.1f MHz\n", kModeNames[m], tStep[m], median(hz[m]) / 1e6);
+        std::printf("CAL_INFO %s %.6f\n", kModeKeys[m], tStep[m]);
+        std::printf("CAL_INFO %sClockHz %.6e\n", kModeKeys[m], median(hz[m]));
+    }
+    const double tS = 8 * (8 * 1024.0 / a.best + 8 * 512.0 / b.best);
+    std::printf("  reads alone against the per-operand rates: %.1f measured, %.1f from ldsA/ldsBTr\n", tStep[1], tS);
+    std::printf("  cost of a phase switch: %.1f cycles ((ping-pong - max(reads, MFMAs)) / 2)\n",
+                (tStep[0] - std::max(tStep[1], tStep[2])) / 2.0);
+    std::printf("CAL_INFO phaseSwitchCycles %.6f\n", (tStep[0] - std::max(tStep[1], tStep[2])) / 2.0);
+    for (int m = 0; m < 4; ++m) ok &= reportConstant(kModeKeys[m], tStep[m], "cycles", st[m]);
+    CAL_HIP_CHECK(hipFree(dOperands));
+    CAL_HIP_CHECK(hipFree(dRefill));
+    CAL_HIP_CHECK(hipFree(dFSink));
+
     std::printf("\nCAL_RESULT smemBytesPerCycle %.6f\n", mix.best);
     std::printf("CAL_RESULT smemSaturationWaves %d\n", mix.bestWaves);
     std::printf("CAL_RESULT ldsControlBytesPerCycle %.6f\n", ctl.best);

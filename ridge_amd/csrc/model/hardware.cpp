@@ -220,6 +220,14 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
         !optionalInteger(kv, "prologueModel", h.prologueModel, err) ||
         !optionalInteger(kv, "pingPongModel", h.pingPongModel, err) ||
         !optionalInteger(kv, "persistentModel", h.persistentModel, err) ||
+        !optionalInteger(kv, "ldsReadModel", h.ldsReadModel, err) ||
+        !optionalNumber(kv, "ldsAReadBytesPerCycle", h.ldsAReadBytesPerCycle, err) ||
+        !optionalNumber(kv, "ldsBTrReadBytesPerCycle", h.ldsBTrReadBytesPerCycle, err) ||
+        !optionalInteger(kv, "clockModel", h.clockModel, err) ||
+        !optionalNumber(kv, "clockRatioHalfCus", h.clockRatio[0], err) ||
+        !optionalNumber(kv, "clockRatioQuarterCus", h.clockRatio[1], err) ||
+        !optionalNumber(kv, "clockRatioEighthCus", h.clockRatio[2], err) ||
+        !optionalNumber(kv, "clockRatioSixteenthCus", h.clockRatio[3], err) ||
         !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
         err = path + ": " + err;
         return false;
@@ -235,6 +243,15 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
     if (h.waveSize <= 0 || h.mmaM <= 0 || h.mmaN <= 0 || h.mmaK <= 0 || h.regGranule <= 0 || h.numXcds <= 0 ||
         h.cBytes <= 0 || h.simdsPerSM < 0 || (h.simdsPerSM > 0 && h.regsPerSimdLane <= 0)) {
         err = path + ": a target-description key is out of range";
+        return false;
+    }
+    if (h.ldsReadModel == 1 && (h.ldsAReadBytesPerCycle <= 0.0 || h.ldsBTrReadBytesPerCycle <= 0.0)) {
+        err = path + ": ldsReadModel 1 needs positive ldsAReadBytesPerCycle and ldsBTrReadBytesPerCycle";
+        return false;
+    }
+    if (h.clockModel == 1 &&
+        (h.clockRatio[0] <= 0.0 || h.clockRatio[1] <= 0.0 || h.clockRatio[2] <= 0.0 || h.clockRatio[3] <= 0.0)) {
+        err = path + ": clockModel 1 needs the four positive clockRatio* keys";
         return false;
     }
     h.calibrated = true;

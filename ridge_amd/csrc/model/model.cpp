@@ -27,6 +27,12 @@
 //                           tiles the kernel actually issues     (reference :91-98)
 //   latency hiding        = hw.warpsNeededToHideIlp8 when a wave carries >= 8
 //                           independent accumulator chains      (reference :72-74)
+//   operand reads         = hw.ldsReadModel 1: A fragments (ds_read_b128) and B
+//                           fragments (transposing ds_read_b64_tr_b16) each at its
+//                           calibrated rate, not one blended rate (reference :45)
+//   last-wave clock       = hw.clockModel 1: a last wave that leaves CUs idle runs
+//                           at the calibrated power-limited clock for its busy
+//                           share of CUs (reference: one clock for every wave)
 //   persistent rows       = hw.persistentModel 1 and cfg.schedule 2: two loader
 //                           waves and the epilogue staging join the workgroup,
 //                           which walks ceil(tiles / slots) tiles and pays one
@@ -105,6 +111,18 @@ double workgroupsByRegisters(const GemmConfig& cfg, const HardwareModel& hw, int
     return std::floor(wavesPerSimd / wavesPerSimdPerCta);
 }
 
+// Loaded-clock ratio for a wave that keeps `busy` (0, 1] of the CUs busy: 1 at
+// a full chip, the calibrated ratios at 1/2, 1/4, 1/8 and 1/16, linear in
+// log2(1 / busy) between them and flat beyond 1/16.
+double clockRatioAtBusyShare(const HardwareModel& hw, double busy) {
+    if (busy >= 1.0) return 1.0;
+    const double x = std::min(4.0, std::log2(1.0 / std::max(busy, 1e-9)));
+    const double pts[5] = {1.0, hw.clockRatio[0], hw.clockRatio[1], hw.clockRatio[2], hw.clockRatio[3]};
+    const int i = std::min(3, int(x));
+    const double f = x - i;
+    return pts[i] + (pts[i + 1] - pts[i]) * f;
+}
+
 }  // namespace
 
 Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
@@ -135,7 +153,12 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         double(cfg.warpM / cfg.mmaM) * (cfg.warpN / cfg.mmaN) * (cfg.BK / cfg.mmaK);
     const double tCompute = mmasPerWarpPerStep * numWarps * hw.mmaCyclesPerInst;
     const double smemBytesPerStep = double(numWarps) * (cfg.warpM + cfg.warpN) * cfg.BK * db;
-    const double tSmem = smemBytesPerStep / hw.smemBytesPerCycle;
+    // ldsReadModel 1: A fragments come from ds_read_b128, B fragments from the
+    // transposing ds_read_b64_tr_b16 at half its rate; each at its calibrated rate.
+    const double tSmem = hw.ldsReadModel == 1
+                             ? double(numWarps) * cfg.BK * db *
+                                   (cfg.warpM / hw.ldsAReadBytesPerCycle + cfg.warpN / hw.ldsBTrReadBytesPerCycle)
+                             : smemBytesPerStep / hw.smemBytesPerCycle;
     // The ping-pong schedule (two waves per SIMD, a ring of three or more stages)
     // runs one wave's operand reads under the other wave's MFMAs, so a K-step
     // costs the longer of the two instead of their sum.
@@ -181,6 +204,17 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const double wavesExact = totalCtas / ctaSlots;
     const double fullWaves = std::ceil(wavesExact);
     const double waveEfficiency = fullWaves > 0.0 ? totalCtas / (fullWaves * ctaSlots) : 1.0;
+    // clockModel 1: under a full matrix load the chip is power-limited, so the
+    // last wave, which leaves CUs idle when the grid does not fill the slots, runs
+    // at a higher clock: the calibrated ratio for the share of CUs it keeps busy.
+    // The run then lasts (fullWaves - 1) + 1 / ratio full-chip wave times.
+    double clockedWaveEfficiency = waveEfficiency;
+    if (hw.clockModel == 1 && fullWaves > 0.0) {
+        const double tailCtas = totalCtas - (fullWaves - 1.0) * ctaSlots;
+        const double busy = std::min(double(hw.numSMs), tailCtas) / double(hw.numSMs);
+        p.tailClockFactor = clockRatioAtBusyShare(hw, busy);
+        clockedWaveEfficiency = totalCtas / (((fullWaves - 1.0) + 1.0 / p.tailClockFactor) * ctaSlots);
+    }
     p.ctaSlots = ctaSlots;
     p.totalCtas = totalCtas;
     p.wavesExact = wavesExact;
@@ -218,7 +252,8 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // Compute ceiling: resident workgroups share the matrix pipes, so occupancy
     // hides latency but never multiplies the peak.
     const double peakTensorTFLOPS = (double(mma.flops) / hw.mmaCyclesPerInst) * hw.clockHz * hw.numSMs / 1e12;
-    const double computeTFLOPS = peakTensorTFLOPS * smEfficiency * occFactor * waveEfficiency * envelopeEfficiency;
+    const double computeTFLOPS =
+        peakTensorTFLOPS * smEfficiency * occFactor * clockedWaveEfficiency * envelopeEfficiency;
     p.peakTensorTFLOPS = peakTensorTFLOPS;
     p.computeTFLOPS = computeTFLOPS;
 

@@ -126,6 +126,7 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     out->reuseTilesM = p.reuseTilesM;
     out->reuseTilesN = p.reuseTilesN;
     out->compulsoryIntensity = p.compulsoryIntensity;
+    out->tailClockFactor = p.tailClockFactor;
     return 0;
 }
 

@@ -371,3 +371,77 @@ def test_mi355x_persistent_occupancy_counts_loaders_and_staging(mi355x):
     # The A100 model has no persistent term: the schedule field is ignored.
     a100 = RM.Hardware("a100")
     assert RM.predict(a100, stages=4, schedule=2, **base) == RM.predict(a100, stages=4, schedule=-1, **base)
+
+
+_CDNA4_JSON = ('{"name": "x", "arch": "gfx950", "numSMs": 256, "clockHz": 2.4e9, "mmaCyclesPerInst": 4, '
+               '"smemBytesPerCycle": 128, "hbmBytesPerSec": 8e12, "regsPerSM": 131072, "smemBytesPerSM": 163840, '
+               '"maxWarpsPerSM": 32, "maxCtasPerSM": 32, "warpsNeededToHide": 8%s}')
+
+
+def test_lds_read_model_prices_each_operand_at_its_rate(tmp_path):
+    """ldsReadModel 1 with A reads at 256 B/cycle and transposing B reads at 128:
+    a 256x256x32 tile of eight wavefront tiles reads 8 x 32 x 2 B = 512 B per
+    wavefront-tile row or column of fragments per K-step, so
+
+      w128x64: 512 x (128/256 + 64/128) = 512       (blended 128 B/cycle: 768)
+      w64x128: 512 x (64/256 + 128/128) = 640       (blended: 768, orientation-blind)
+
+    and a model without the two rates is refused."""
+    f = tmp_path / "lds.json"
+    f.write_text(_CDNA4_JSON % ', "ldsReadModel": 1, "ldsAReadBytesPerCycle": 256, "ldsBTrReadBytesPerCycle": 128')
+    hw = RM.Hardware(str(f))
+    cfg = dict(M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, stages=2, regsPerThread=197)
+    assert RM.predict(hw, warpM=128, warpN=64, **cfg)["tSmemCycles"] == pytest.approx(512.0)
+    assert RM.predict(hw, warpM=64, warpN=128, **cfg)["tSmemCycles"] == pytest.approx(640.0)
+    blended = tmp_path / "blend.json"
+    blended.write_text(_CDNA4_JSON % "")
+    for wm, wn in ((128, 64), (64, 128)):
+        assert RM.predict(RM.Hardware(str(blended)), warpM=wm, warpN=wn, **cfg)["tSmemCycles"] == pytest.approx(768.0)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "ldsReadModel": 1, "ldsAReadBytesPerCycle": 256')
+    with pytest.raises(ValueError, match="ldsReadModel 1"):
+        RM.Hardware(str(bad))
+
+
+def test_clock_model_runs_the_last_wave_at_its_busy_share_clock(tmp_path):
+    """clockModel 1 with ratios 1.25 / 1.3 / 1.3 / 1.3 at 1/2 .. 1/16 of the CUs
+    busy. 256x256x32 tiles, 128x64 wavefront tiles, 4 stages: 128 KiB of LDS, one
+    workgroup per CU, 256 slots.
+
+      256 tiles: one full wave, busy 1 -> ratio 1, compute unchanged
+      128 tiles: busy 1/2 -> 1.25; waves 128 / ((0 + 1/1.25) x 256) = 0.625
+                 against the quantisation's 0.5: compute x 1.25
+      192 tiles: busy 3/4 -> x = log2(4/3) = 0.415037, ratio 1 + 0.25 x 0.415037
+      320 tiles: two waves, the last with 64 busy (1/4) -> 1.3;
+                 320 / ((1 + 1/1.3) x 256) = 0.706522 against 0.625
+        8 tiles: busy 1/32, flat beyond 1/16 -> 1.3
+    """
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % (', "clockModel": 1, "clockRatioHalfCus": 1.25, "clockRatioQuarterCus": 1.3, '
+                                 '"clockRatioEighthCus": 1.3, "clockRatioSixteenthCus": 1.3'))
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % "")
+    hw_on, hw_off = RM.Hardware(str(on)), RM.Hardware(str(off))
+    tile = dict(K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=4, regsPerThread=197)
+    cases = [((4096, 4096), 1.0, 1.0), ((2048, 4096), 1.25, 0.625),
+             ((3072, 4096), 1 + 0.25 * math.log2(4 / 3), None), ((5120, 4096), 1.3, 320 / ((1 + 1 / 1.3) * 256)),
+             ((512, 1024), 1.3, None)]
+    for (m, n), ratio, clocked in cases:
+        p_on = RM.predict(hw_on, M=m, N=n, **tile)
+        p_off = RM.predict(hw_off, M=m, N=n, **tile)
+        assert p_on["ctasPerSM"] == 1
+        assert p_on["tailClockFactor"] == pytest.approx(ratio, rel=1e-12)
+        assert p_off["tailClockFactor"] == 1.0
+        # The quantisation figure (and so the label) is the reference's either way.
+        assert p_on["waveEfficiency"] == p_off["waveEfficiency"]
+        if clocked is not None:
+            assert p_on["computeTFLOPS"] / p_off["computeTFLOPS"] == pytest.approx(
+                clocked / p_off["waveEfficiency"], rel=1e-12)
+    # one busy wave of a partly filled grid: compute scales by the ratio itself
+    p_on = RM.predict(hw_on, M=2048, N=4096, **tile)
+    p_off = RM.predict(hw_off, M=2048, N=4096, **tile)
+    assert p_on["computeTFLOPS"] / p_off["computeTFLOPS"] == pytest.approx(1.25, rel=1e-12)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "clockModel": 1, "clockRatioHalfCus": 1.25')
+    with pytest.raises(ValueError, match="clockModel 1"):
+        RM.Hardware(str(bad))
