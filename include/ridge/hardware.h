@@ -68,6 +68,11 @@ struct HardwareModel {
                                      //    idle runs at clockHz x clockRatio for its busy share
     double clockRatio[4] = {0.0, 0.0, 0.0, 0.0};  // [CAL] loaded clock with 1/2, 1/4, 1/8, 1/16 of the
                                                   // CUs busy, over the clock with all of them busy
+    int l2StreamModel = 0;           // 0: the HBM roofline alone bounds the memory side (reference)
+                                     // 1: tile loads that the L2s serve (every workgroup re-reading
+                                     //    a shared panel) take their own time at
+                                     //    l2HitBytesPerCycle x clockHz, in series with the HBM stream
+    double l2HitBytesPerCycle = 0.0; // [CAL] whole GPU, per shader cycle, reads served by the XCDs' L2s
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -51,6 +51,9 @@ struct Prediction {
 
     // Power-limited clock (clockModel 1; 1.0 otherwise).
     double tailClockFactor = 1.0;      // clock of the last wave over the full-chip clock
+
+    // L2 stream (l2StreamModel 1; 0 otherwise).
+    double l2HitBytes = 0.0;           // tile-load bytes served by the L2s, not HBM
 };
 
 }  // namespace ridge

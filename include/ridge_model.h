@@ -42,6 +42,7 @@ typedef struct ridge_model_prediction {
     double tComputeCycles, tSmemCycles, tStepCycles;
     double reuseTilesM, reuseTilesN, compulsoryIntensity;
     double tailClockFactor;  /* clock of the last wave over the full-chip clock (clockModel 1) */
+    double l2HitBytes;       /* tile-load bytes served by the L2s (l2StreamModel 1) */
 } ridge_model_prediction_t;
 
 /* Default config (the reference's GemmConfig defaults, config.h:18-39). */

@@ -19,8 +19,9 @@ MI355X differences from the reference driver:
   * the JSON carries the CDNA4 target description ("arch": "gfx950") and the
     extra measured keys (MALL bandwidth, LDS control and per-pattern rates);
   * the chip is power-limited, so cal-mma also measures the loaded clock with
-    1/2 .. 1/16 of the CUs busy (clockRatio*: the model's clockModel 1), and the
-    per-operand LDS rates feed ldsReadModel 1;
+    1/2 .. 1/16 of the CUs busy (clockRatio*: the model's clockModel 1), the
+    per-operand LDS rates feed ldsReadModel 1, and cal-hbm-bw's L2-resident read
+    (l2HitBytesPerCycle) feeds l2StreamModel 1;
   * cal-smem-bw's ping-pong skeleton figures (reads under MFMAs, with and without
     the GEMM's direct-to-LDS refill) are kept in the JSON as a record.
 """
@@ -98,6 +99,10 @@ def band_check(res, spec):
     ok &= check("hbmBytesPerSec", res["hbmBytesPerSec"] / 1e12, spec["hbm_bytes_per_sec"] * 0.60 / 1e12,
                 spec["hbm_bytes_per_sec"] * 1.02 / 1e12, "TB/s", "above spec would mean the MALL, not HBM")
     ok &= check("warpsNeededToHide", res["warpsNeededToHide"], 1, 32, "waves/CU")
+    # The L2s serve faster than HBM (at the loaded clock); 8 XCDs x 16 channels x
+    # 128 B per cycle is the ceiling.
+    ok &= check("l2HitBytesPerCycle", res["l2HitBytesPerCycle"], res["hbmBytesPerSec"] / res["clockHz"],
+                8 * 16 * 128 * 1.05, "B/cycle", "above HBM at the loaded clock, below the L2 channels' peak")
     # A partly busy chip clocks at least as fast as a full one (within noise) and
     # never past the engine clock's ceiling.
     ceiling = spec["clock_hz"] * 1.05 / res["clockHz"]
@@ -159,6 +164,8 @@ def hardware_json(res, spec, arch):
         "mfma32x32x16ClockHz": res.get("mfma32x32x16ClockHz", 0.0),
         "ldsReadModel": 1,
         "clockModel": 1,
+        "l2StreamModel": 1,
+        "l2HitBytesPerCycle": res["l2HitBytesPerCycle"],
     }
     for key in CLOCK_RATIO_KEYS:
         out[key] = res[key]
@@ -204,7 +211,7 @@ def main(argv=None):
     spec = SPECS[arch]
     required = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
                 "smemBytesPerCycle", "ldsControlBytesPerCycle", "ldsAReadBytesPerCycle", "ldsBTrReadBytesPerCycle",
-                "hbmBytesPerSec", "warpsNeededToHide"] + CLOCK_RATIO_KEYS
+                "hbmBytesPerSec", "l2HitBytesPerCycle", "warpsNeededToHide"] + CLOCK_RATIO_KEYS
     missing = [k for k in required if k not in results]
     if missing:
         sys.exit("benchmarks did not report: %s" % ", ".join(missing))

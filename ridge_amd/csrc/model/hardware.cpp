@@ -228,6 +228,8 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
         !optionalNumber(kv, "clockRatioQuarterCus", h.clockRatio[1], err) ||
         !optionalNumber(kv, "clockRatioEighthCus", h.clockRatio[2], err) ||
         !optionalNumber(kv, "clockRatioSixteenthCus", h.clockRatio[3], err) ||
+        !optionalInteger(kv, "l2StreamModel", h.l2StreamModel, err) ||
+        !optionalNumber(kv, "l2HitBytesPerCycle", h.l2HitBytesPerCycle, err) ||
         !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
         err = path + ": " + err;
         return false;
@@ -252,6 +254,10 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
     if (h.clockModel == 1 &&
         (h.clockRatio[0] <= 0.0 || h.clockRatio[1] <= 0.0 || h.clockRatio[2] <= 0.0 || h.clockRatio[3] <= 0.0)) {
         err = path + ": clockModel 1 needs the four positive clockRatio* keys";
+        return false;
+    }
+    if (h.l2StreamModel == 1 && h.l2HitBytesPerCycle <= 0.0) {
+        err = path + ": l2StreamModel 1 needs a positive l2HitBytesPerCycle";
         return false;
     }
     h.calibrated = true;

@@ -33,6 +33,9 @@
 //   last-wave clock       = hw.clockModel 1: a last wave that leaves CUs idle runs
 //                           at the calibrated power-limited clock for its busy
 //                           share of CUs (reference: one clock for every wave)
+//   L2 stream             = hw.l2StreamModel 1: tile loads the L2s serve take
+//                           their own time, in series with the HBM stream
+//                           (reference: the HBM roofline alone)
 //   persistent rows       = hw.persistentModel 1 and cfg.schedule 2: two loader
 //                           waves and the epilogue staging join the workgroup,
 //                           which walks ceil(tiles / slots) tiles and pays one
@@ -342,6 +345,19 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     p.baseIntensity = baseIntensity;
     p.arithmeticIntensity = arithmeticIntensity;
     p.hbmTFLOPS = hw.hbmBytesPerSec * arithmeticIntensity / 1e12;
+    if (hw.l2StreamModel == 1) {
+        // Every workgroup loads its (BM + BN) x K panels; the share that HBM does
+        // not supply (a panel re-read by the workgroups of one XCD) is served by
+        // that XCD's L2, and a load-only kernel with the GEMM's streams takes the
+        // sum of the two stream times, not the larger.
+        const double flops = 2.0 * double(cfg.M) * double(cfg.N) * double(cfg.K);
+        const double hbmBytes = flops / arithmeticIntensity;
+        const double tileBytes = flops / baseIntensity;
+        const double seconds = hbmBytes / hw.hbmBytesPerSec +
+                               std::max(0.0, tileBytes - hbmBytes) / (hw.l2HitBytesPerCycle * hw.clockHz);
+        p.l2HitBytes = std::max(0.0, tileBytes - hbmBytes);
+        p.hbmTFLOPS = flops / seconds / 1e12;
+    }
 
     // The label names the derating furthest from 1.0 (reference :129-143).
     p.predictedTFLOPS = std::min(computeTFLOPS, p.hbmTFLOPS);

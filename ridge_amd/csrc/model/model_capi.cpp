@@ -127,6 +127,7 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     out->reuseTilesN = p.reuseTilesN;
     out->compulsoryIntensity = p.compulsoryIntensity;
     out->tailClockFactor = p.tailClockFactor;
+    out->l2HitBytes = p.l2HitBytes;
     return 0;
 }
 

@@ -445,3 +445,36 @@ def test_clock_model_runs_the_last_wave_at_its_busy_share_clock(tmp_path):
     bad.write_text(_CDNA4_JSON % ', "clockModel": 1, "clockRatioHalfCus": 1.25')
     with pytest.raises(ValueError, match="clockModel 1"):
         RM.Hardware(str(bad))
+
+
+def test_l2_stream_model_adds_the_l2_served_tile_loads(tmp_path):
+    """l2StreamModel 1 at 16384 B/cycle and 2.4 GHz (39.3216 TB/s), HBM 8 TB/s.
+    16384 x 128 x 8192 with 128x64x64 tiles, groupM 8: 128 x 2 = 256 tiles, one per
+    CU. Every tile loads (128 + 64) x 8192 x 2 B = 3 MiB: 768 MiB in all. Per XCD
+    (32 tiles, 16 row panels x 2 column panels) the launch order fetches 16 A and
+    2 B panels once, 8 x (16 x 128 + 2 x 64) x 8192 x 2 B = 285,212,672 B from HBM,
+    which is also what l2ReuseModel 2 charges. The rest, 805,306,368 - 285,212,672
+    = 520,093,696 B, are L2 hits:
+
+      t = 285212672 / 8e12 + 520093696 / 39.3216e12 = 35.652 us + 13.227 us
+      hbmTFLOPS = 2 x 16384 x 128 x 8192 / t = 703.0 (HBM alone: 963.8)"""
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % ', "l2StreamModel": 1, "l2HitBytesPerCycle": 16384, "l2ReuseModel": 2')
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % ', "l2ReuseModel": 2')
+    cfg = dict(M=16384, N=128, K=8192, BM=128, BN=64, BK=64, warpM=64, warpN=32, stages=6, regsPerThread=131,
+               groupM=8, schedule=2)
+    p_on = RM.predict(RM.Hardware(str(on)), **cfg)
+    p_off = RM.predict(RM.Hardware(str(off)), **cfg)
+    flops = 2.0 * 16384 * 128 * 8192
+    assert p_off["l2HitBytes"] == 0.0
+    assert flops / p_off["arithmeticIntensity"] == pytest.approx(285212672.0, rel=1e-12)
+    assert p_on["l2HitBytes"] == pytest.approx(520093696.0, rel=1e-12)
+    t = 285212672.0 / 8e12 + 520093696.0 / (16384 * 2.4e9)
+    assert p_on["hbmTFLOPS"] == pytest.approx(flops / t / 1e12, rel=1e-12)
+    assert p_on["hbmTFLOPS"] == pytest.approx(703.0, abs=0.05)
+    assert p_off["hbmTFLOPS"] == pytest.approx(963.8, abs=0.05)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "l2StreamModel": 1')
+    with pytest.raises(ValueError, match="l2StreamModel 1"):
+        RM.Hardware(str(bad))
