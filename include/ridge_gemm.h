@@ -116,6 +116,11 @@ int ridge_blaslt_gemm(void* handle, const void* A, const void* B, void* C, int M
 /* Library identification for logs: "ridge_gemm gfx950 <build info>". */
 const char* ridge_gemm_build_info(void);
 
+/* sizeof(ridge_gemm_variant_t) as this library was built, so a binding that
+ * declares the struct itself (ctypes, cgo, JNA) can refuse a layout that
+ * disagrees. No counterpart in the reference (its callers include its header). */
+size_t ridge_gemm_variant_struct_size(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,12 @@ int ridge_model_predict(const void* hw, const ridge_model_config_t* cfg, ridge_m
 /* Label string of a bottleneck code ("TENSOR_CORE", ..., "DOES_NOT_FIT"). */
 const char* ridge_model_bottleneck_name(int code);
 
+/* sizeof the two structs as this library was built, so a binding that declares
+ * them itself (ctypes, cgo, JNA) can refuse a layout that disagrees. No
+ * counterpart in the reference (its callers compile against its headers). */
+size_t ridge_model_config_size(void);
+size_t ridge_model_prediction_size(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -193,6 +193,8 @@ size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {
     return s.size();
 }
 
+size_t ridge_gemm_variant_struct_size(void) { return sizeof(ridge_gemm_variant_t); }
+
 const char* ridge_gemm_build_info(void) {
     return "ridge_gemm gfx950 mfma_f32_16x16x32_f16, direct-to-LDS ring, tr16 B reads, xcd+groupM order, "
            "ping-pong schedule for 8-wave rings of 3+ stages, persistent store-behind rows with loader waves";

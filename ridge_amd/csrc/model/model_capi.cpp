@@ -131,6 +131,10 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     return 0;
 }
 
+size_t ridge_model_config_size(void) { return sizeof(ridge_model_config_t); }
+
+size_t ridge_model_prediction_size(void) { return sizeof(ridge_model_prediction_t); }
+
 const char* ridge_model_bottleneck_name(int code) {
     if (code < 0 || code > int(Bottleneck::DoesNotFit)) return "UNKNOWN";
     return toString(static_cast<Bottleneck>(code));

@@ -125,6 +125,12 @@ def lib():
     L.ridge_blaslt_gemm.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]
     L.ridge_gemm_build_info.restype = ctypes.c_char_p
     L.ridge_gemm_build_info.argtypes = []
+    L.ridge_gemm_variant_struct_size.restype = c_size_t
+    L.ridge_gemm_variant_struct_size.argtypes = []
+    if L.ridge_gemm_variant_struct_size() != ctypes.sizeof(_VariantStruct):
+        raise RidgeGemmError("ridge_gemm_variant_t is %d bytes in %s but %d in this binding: rebuild or update "
+                             "_VariantStruct" % (L.ridge_gemm_variant_struct_size(), LIB_PATH,
+                                                 ctypes.sizeof(_VariantStruct)))
     _lib = L
     return L
 

@@ -63,6 +63,12 @@ def lib():
     L.ridge_model_predict.restype = ctypes.c_int
     L.ridge_model_bottleneck_name.argtypes = [ctypes.c_int]
     L.ridge_model_bottleneck_name.restype = ctypes.c_char_p
+    for fn, struct in ((L.ridge_model_config_size, _Config), (L.ridge_model_prediction_size, _Prediction)):
+        fn.argtypes = []
+        fn.restype = ctypes.c_size_t
+        if fn() != ctypes.sizeof(struct):
+            raise RuntimeError("%s: %d bytes in %s but %d in this binding" % (fn.__name__, fn(), LIB_PATH,
+                                                                             ctypes.sizeof(struct)))
     _lib = L
     return L
 

@@ -108,3 +108,16 @@ def test_persistent_rows_are_labelled():
     ps = [v for v in G.variants() if v.schedule == 2]
     assert ps and all(v.label().endswith(" persistent") and v.schedule_name == "persistent" for v in ps)
     assert all(not v.label().endswith("persistent") for v in G.variants() if v.schedule != 2)
+
+
+def test_binding_struct_layouts_match_the_libraries():
+    """The ctypes stubs declare the C structs themselves; each library reports its
+    own sizeof, and loading refuses a disagreement (a short struct would be
+    overwritten past its end by the library)."""
+    from ridge_amd import model as RM
+    assert G.lib().ridge_gemm_variant_struct_size() == ctypes.sizeof(G._VariantStruct)
+    L = RM.lib()
+    assert L.ridge_model_config_size() == ctypes.sizeof(RM._Config)
+    assert L.ridge_model_prediction_size() == ctypes.sizeof(RM._Prediction)
+    # The prediction ends with the two gfx950 fields, after the reference's.
+    assert [f for f, _ in RM._Prediction._fields_][-2:] == ["tailClockFactor", "l2HitBytes"]
