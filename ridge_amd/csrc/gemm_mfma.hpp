@@ -31,8 +31,9 @@
 //    and lane i receives B[k0 .. k0 + 3][n0 + i].
 //  * The operands are swapped (B fragment in the instruction's A slot), which
 //    yields the transposed accumulator: lane l holds C[m0 + l%16][n0 + 4(l/16) + r]
-//    in acc[r]. Four consecutive columns per lane let the epilogue write 8-byte
-//    FP16 stores with no LDS round trip.
+//    in acc[r]. The epilogue converts those four columns to 8 bytes of FP16 in an
+//    LDS staging region and reads whole rows back, so every global store is 16
+//    bytes per lane (storeStaged).
 //  * Workgroup order: the hardware deals workgroups round-robin over the 8 XCDs,
 //    each with its own L2. xcdRemap makes the workgroups of one XCD a contiguous
 //    range of the logical order, and the GroupM mapping of that logical order
