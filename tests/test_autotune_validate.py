@@ -91,3 +91,21 @@ def test_measured_mi355x_sweep_is_the_registered_cross_product():
                                                                               "mi355x-registered.csv")),
                                           V.load_variant_table())
     assert not missing and not extra
+
+
+@pytest.mark.parametrize("name", ["mi355x.csv", "mi355x-replicate.csv"])
+def test_mi355x_pruner_meets_the_target_on_each_measurement(name):
+    """The calibrated model prunes the MI355X sweep to within the BASELINE target
+    (mean regret <= 2% at k = 10) on the committed measurement and on an
+    independent re-measurement taken on another box; both cover the registered
+    cross product."""
+    path = os.path.join(ROOT, "data", "measured", name)
+    rows = list(csv.DictReader(l for l in open(path) if not l.startswith("#")))
+    missing, extra = V.cross_product_gate(rows, V.load_registered(os.path.join(ROOT, "data", "sweep",
+                                                                              "mi355x-registered.csv")),
+                                          V.load_variant_table())
+    assert not missing and not extra
+    table, total, nshapes, per_shape = AT.evaluate(path, os.path.join(ROOT, "data", "hardware", "mi355x.json"))
+    assert (total, nshapes) == (336, 14)
+    k10 = [r for r in table if r["k"] == 10][0]
+    assert k10["mean_regret"] <= 2.0
