@@ -28,6 +28,9 @@ bounded sample of the same 4096^3 workload (a block of output rows, about 10 s o
 work), reported in TFLOP/s with the thread count used (the cores this process may
 run on, at most 16).
 
+model: the calibrated cost model's prediction for the measured variant and shape
+(TFLOP/s, label, error against `value`), read from data/hardware/mi355x.json.
+
 autotune: the metric's second half, the mean top-10 regret of the model-pruned
 autotuner, is computed from the committed measured sweep (data/measured/mi355x.csv,
 14 shapes x 24 variants) and the committed calibration (data/hardware/mi355x.json)
@@ -202,6 +205,21 @@ def autotune_regret(k=10):
     return {"top_k": k, "mean_regret_pct": round(row["mean_regret"], 3), "max_regret_pct": round(row["max_regret"], 3),
             "exact_hits": row["hits"], "shapes": shapes, "configs": total,
             "benchmarks_vs_exhaustive": round(row["reduction"], 2), "source": "data/measured/mi355x.csv"}
+
+
+def model_prediction(v, M, N, K, measured):
+    """The calibrated cost model's prediction for the variant this run measured:
+    TFLOP/s, bottleneck label and the error against the measurement."""
+    try:
+        from ridge_amd import model as RM
+        p = RM.predict(RM.Hardware(HARDWARE_JSON), M=M, N=N, K=K, BM=v.BM, BN=v.BN, BK=v.BK, warpM=v.WM,
+                       warpN=v.WN, stages=v.stages, regsPerThread=v.regsPerThread, groupM=v.groupM,
+                       schedule=v.schedule)
+    except Exception as e:  # the model library is part of the build; report its absence
+        return {"error": "%s" % e}
+    return {"predicted_tflops": round(p["predictedTFLOPS"], 1), "label": p["bottleneck"],
+            "error_pct": round((p["predictedTFLOPS"] - measured) / measured * 100, 1),
+            "hardware": os.path.relpath(HARDWARE_JSON, ROOT)}
 
 
 def cpu_baseline(M, N, K, seconds=10.0):
@@ -422,6 +440,7 @@ def main():
         out["cold"] = cold
     out["device"] = device
     out["autotune"] = autotune_regret(10)
+    out["model"] = model_prediction(v, M, N, K, value)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)
         out["cpu_baseline_naive_1core"] = cpu_baseline_naive_1core()
