@@ -117,6 +117,11 @@ def band_check(res, spec):
 
 CLOCK_RATIO_KEYS = ["clockRatioHalfCus", "clockRatioQuarterCus", "clockRatioEighthCus", "clockRatioSixteenthCus"]
 
+# What the four benchmarks must report for a JSON to be written.
+REQUIRED_KEYS = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
+                 "smemBytesPerCycle", "ldsControlBytesPerCycle", "ldsAReadBytesPerCycle", "ldsBTrReadBytesPerCycle",
+                 "hbmBytesPerSec", "l2HitBytesPerCycle", "warpsNeededToHide"] + CLOCK_RATIO_KEYS
+
 # Figures of the ping-pong skeleton (cal-smem-bw), kept in the JSON as a record;
 # the model reads none of them.
 SKELETON_KEYS = ["pingPongStepCycles", "pingPongReadCycles", "pingPongMfmaCycles", "pingPongRefillStepCycles",
@@ -209,10 +214,7 @@ def main(argv=None):
     if arch not in SPECS:
         sys.exit("no datasheet entry for %s: add one to SPECS rather than reusing another card's" % arch)
     spec = SPECS[arch]
-    required = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
-                "smemBytesPerCycle", "ldsControlBytesPerCycle", "ldsAReadBytesPerCycle", "ldsBTrReadBytesPerCycle",
-                "hbmBytesPerSec", "l2HitBytesPerCycle", "warpsNeededToHide"] + CLOCK_RATIO_KEYS
-    missing = [k for k in required if k not in results]
+    missing = [k for k in REQUIRED_KEYS if k not in results]
     if missing:
         sys.exit("benchmarks did not report: %s" % ", ".join(missing))
 
