@@ -125,6 +125,23 @@ def test_headline_4096_exact_integers_and_identity(key):
     assert torch.equal(C.view(torch.int16), Bu.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 128), (16384, 128, 8192)])
+def test_baseline_small_k_and_tall_skinny_exact_every_variant(M, N, K):
+    """The two HBM-bound BASELINE configs at full size, every variant that divides
+    them (the persistent rows among them), on integers in [-2, 2]: every partial
+    sum is exact in FP32 (|C| <= 4K <= 32768), so the FP16 output must equal the
+    exact product rounded once, bit for bit."""
+    Ab, Bb, want = _exact_case(M, N, K, -2, 2, M ^ (N << 4) ^ K)
+    A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+    rows = [v for v in G.variants() if v.divides(M, N, K)]
+    assert any(v.schedule == 2 for v in rows)
+    for v in rows:
+        print("  %s %dx%dx%d" % (v.label(), M, N, K), flush=True)
+        got = _bits(_run(v.index, A, B, M, N, K))
+        bad = int(np.count_nonzero(got != want))
+        assert bad == 0, "%s: %d of %d outputs differ" % (v.label(), bad, M * N)
+
+
 def _persistent_edge_shapes(v):
     """Shapes that drive the persistent schedule's control flow to its edges."""
     BM, BN, BK, S = v.BM, v.BN, v.BK, v.stages
