@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -27,16 +28,19 @@ enum Schedule { kUniform = 0, kPingPong = 1, kPersistent = 2 };
 constexpr bool usesPingPong(int waves, int stages) { return waves == 8 && stages >= 3; }
 
 // Workgroups of `kernel` resident on the current device at once (CUs x
-// workgroups per CU), cached per device: the persistent grid. The host side is
-// single-threaded, as the reference's (the table is an immutable static).
-int residentSlots(const void* kernel, int threads, int& cache) {
-    if (cache > 0) return cache;
+// workgroups per CU), cached per device: the persistent grid. Launches from
+// several host threads may fill the cache concurrently; they compute the same
+// value, and the atomic makes the store and the loads well defined.
+int residentSlots(const void* kernel, int threads, std::atomic<int>& cache) {
+    const int cached = cache.load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
     int dev = 0, cus = 0, perCu = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, kernel, threads, 0) != hipSuccess) return 0;
-    cache = cus * (perCu > 0 ? perCu : 1);
-    return cache;
+    const int slots = cus * (perCu > 0 ? perCu : 1);
+    cache.store(slots, std::memory_order_relaxed);
+    return slots;
 }
 
 constexpr int kMaxDevices = 64;
@@ -44,7 +48,7 @@ constexpr int kMaxDevices = 64;
 template <int BM, int BN, int BK, int WM, int WN, int S, int G>
 hipError_t launchPersistent(const void* A, const void* B, void* C, int M, int N, int K, hipStream_t stream) {
     using P = ridge::PersistentTraits<BM, BN, BK, WM, WN, S, G>;
-    static int slots[kMaxDevices];
+    static std::atomic<int> slots[kMaxDevices];
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;

@@ -248,3 +248,37 @@ def test_registered_sweep_shapes_every_variant(M, N, K):
         ok, frob, mx, ne = O.passes(got, ref, 1.0, 1.0, K)
         assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
         del C
+
+
+def test_concurrent_host_threads_launch_persistent_rows():
+    """Four host threads, each with its own stream and buffers, launch a persistent
+    row 20 times at once (the first launches fill the per-device grid cache
+    concurrently); every result is the exact product of small integers."""
+    import threading
+    v = [w for w in G.variants() if w.schedule == 2][0]
+    M, N, K = 8 * v.BM, 4 * v.BN, 4 * v.BK
+    Ab, Bb, want = _exact_case(M, N, K, -3, 3, 77)
+    jobs = []
+    for t in range(4):
+        A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+        C = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+        jobs.append((A, B, C, torch.cuda.Stream()))
+    torch.cuda.synchronize()
+    errors = []
+
+    def work(A, B, C, s):
+        for _ in range(20):
+            rc = G.launch(v.index, A, B, C, M, N, K, s)
+            if rc != 0:
+                errors.append(rc)
+                return
+
+    threads = [threading.Thread(target=work, args=j) for j in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    torch.cuda.synchronize()
+    assert not errors
+    for (_, _, C, _) in jobs:
+        assert np.array_equal(_bits(C), want)
