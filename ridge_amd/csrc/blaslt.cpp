@@ -113,9 +113,15 @@ int ridge_blaslt_prepare(void* handle, const void* A, const void* B, void* C, in
         return rc;
     }
     hipblasLtMatmulPreference_t pref = nullptr;
-    hipblasLtMatmulPreferenceCreate(&pref);
+    hipblasStatus_t pst = hipblasLtMatmulPreferenceCreate(&pref);
     const uint64_t ws = kWorkspaceBytes;
-    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+    if (pst == HIPBLAS_STATUS_SUCCESS)
+        pst = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+    if (pst != HIPBLAS_STATUS_SUCCESS) {
+        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        destroyPlan(p);
+        return (int)pst;
+    }
     if (candidates < 1) candidates = 1;
     std::vector<hipblasLtMatmulHeuristicResult_t> res(candidates);
     int returned = 0;
