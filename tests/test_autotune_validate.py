@@ -109,3 +109,17 @@ def test_mi355x_pruner_meets_the_target_on_each_measurement(name):
     assert (total, nshapes) == (336, 14)
     k10 = [r for r in table if r["k"] == 10][0]
     assert k10["mean_regret"] <= 2.0
+
+
+def test_error_classes_by_resident_waves_hand_case():
+    """Two 4-wave rows with two resident workgroups (2 waves per SIMD) and one
+    8-wave ping-pong row with one (2 per SIMD, its own class): per-class mean of
+    |err| and of signed err."""
+    rows = [
+        dict(BM="128", BN="128", WM="64", WN="64", pred_ctas_per_sm="2", schedule="0", _abs=10.0, _signed=10.0),
+        dict(BM="128", BN="128", WM="64", WN="64", pred_ctas_per_sm="2", schedule="0", _abs=20.0, _signed=-20.0),
+        dict(BM="256", BN="256", WM="128", WN="64", pred_ctas_per_sm="1", schedule="1", _abs=5.0, _signed=5.0),
+    ]
+    got = V.error_by_resident_waves(rows)
+    assert got == {(2.0, "4-wave uniform"): (2, 15.0, -5.0), (2.0, "8-wave ping-pong"): (1, 5.0, 5.0)}
+    assert V.error_by_resident_waves([dict(BM="1")]) == {}
