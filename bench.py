@@ -344,9 +344,16 @@ def main():
 
     blas = None
     blas_before = blas_after = None
+    blas_error = None
     if not args.no_blaslt:
-        blas = G.BlasLt()
-        blas.prepare(A, B, C, M, N, K, candidates=16, iters=20, stream=stream)
+        # The comparator is context, not the measurement: if hipBLASLt cannot
+        # serve the shape, the line still reports `value` and says why.
+        try:
+            blas = G.BlasLt()
+            blas.prepare(A, B, C, M, N, K, candidates=16, iters=20, stream=stream)
+        except G.RidgeGemmError as e:
+            blas, blas_error = None, str(e)
+    if blas is not None:
 
         def blas_step():
             blas.gemm(A, B, C, M, N, K, stream=stream)
@@ -397,8 +404,13 @@ def main():
                 "sets": n_sets, "set_bytes": set_bytes, "launches": cold_steps,
                 "roofline": roofline(M, N, K, cold_ms, None)}
         if blas is not None:
-            blas = G.BlasLt()
-            blas.prepare(A, B, C, M, N, K, candidates=16, iters=20, stream=stream)
+            try:
+                blas = G.BlasLt()
+                blas.prepare(A, B, C, M, N, K, candidates=16, iters=20, stream=stream)
+            except G.RidgeGemmError as e:
+                blas = None
+                cold["hipblaslt_error"] = str(e)
+        if blas is not None:
 
             def make_blas_step(a, b, c):
                 return lambda: blas.gemm(a, b, c, M, N, K, stream=stream)
@@ -430,6 +442,8 @@ def main():
         "frac_of_mfma_peak": round(value / PEAK_FP16_TFLOPS, 4),
         "roofline": roofline(M, N, K, per_launch_ms, traffic),
     }
+    if blas_error is not None:
+        out["hipblaslt"] = {"error": blas_error}
     if blas_before is not None:
         best = max(blas_before, blas_after)
         out["hipblaslt"] = {"tflops": round(best, 3), "before": round(blas_before, 3),
