@@ -3,6 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant BM,BN,BK,WM,WN,S,G]
                     [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt] [--no-cold]
+                    [--operands uniform|zeros|ones]
                     [--allow-partitioned]
     python bench.py --mode copy     # plain device copy of known size, for scaling
                                     # rocprofv3 FETCH_SIZE / WRITE_SIZE counters
@@ -287,6 +288,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--variant", default=",".join(str(x) for x in DEFAULT_VARIANT))
     ap.add_argument("--shape", default=",".join(str(x) for x in DEFAULT_SHAPE))
+    ap.add_argument("--operands", default="uniform", choices=["uniform", "zeros", "ones"],
+                    help="operand data; anything but the default is a power-limit probe, not the metric")
     ap.add_argument("--warm-seconds", type=float, default=3.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-blaslt", action="store_true")
@@ -324,8 +327,17 @@ def main():
     A = torch.empty((M, K), dtype=torch.float16, device=dev)
     B = torch.empty((K, N), dtype=torch.float16, device=dev)
     C = torch.empty((M, N), dtype=torch.float16, device=dev)
-    G.fill_uniform(A, 1)
-    G.fill_uniform(B, 2)
+    def fill(a, b):
+        if args.operands == "uniform":
+            G.fill_uniform(a, 1)
+            G.fill_uniform(b, 2)
+        else:
+            # Constant operands toggle no bits from one MFMA to the next; the
+            # same instructions then draw less power (1/64 keeps C exact).
+            a.fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
+            b.fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
+
+    fill(A, B)
     torch.cuda.synchronize()
     flops = 2.0 * M * N * K
 
@@ -386,8 +398,7 @@ def main():
         for i in range(1, n_sets):
             Ai = torch.empty_like(A)
             Bi = torch.empty_like(B)
-            G.fill_uniform(Ai, 1)
-            G.fill_uniform(Bi, 2)
+            fill(Ai, Bi)
             sets.append((Ai, Bi, torch.empty_like(C)))
         torch.cuda.synchronize()
 
@@ -436,7 +447,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic: A, B ~ U[-1,1) FP16 from splitmix64 seeds 1 and 2, generated on the device",
+        "data": ("synthetic: A, B ~ U[-1,1) FP16 from splitmix64 seeds 1 and 2, generated on the device"
+                 if args.operands == "uniform" else
+                 "POWER-LIMIT PROBE, not the metric: every element of A and B is %s"
+                 % ("0" if args.operands == "zeros" else "1/64")),
         "config": {"workload": "FP16 GEMM M=%d N=%d K=%d, row-major A/B/C, FP32 accumulate, FP16 C" % (M, N, K),
                    "variant": v.label(), "parallelism": "single GPU"},
         "frac_of_mfma_peak": round(value / PEAK_FP16_TFLOPS, 4),
