@@ -73,6 +73,11 @@ struct HardwareModel {
                                      //    a shared panel) take their own time at
                                      //    l2HitBytesPerCycle x clockHz, in series with the HBM stream
     double l2HitBytesPerCycle = 0.0; // [CAL] whole GPU, per shader cycle, reads served by the XCDs' L2s
+    int powerModel = 0;              // 0: the loaded clock of a pure MFMA stream, clockHz (reference)
+                                     // 1: a row that keeps the matrix pipes busy a share u of the
+                                     //    time runs at clockHz x (1 - (1 - loadedClockRatio) u)
+    double loadedClockRatio = 0.0;   // [CAL] clock of the ping-pong skeleton with the GEMM's reads
+                                     // and refill over that of its MFMAs alone (cal-smem-bw)
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

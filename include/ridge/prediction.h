@@ -54,6 +54,9 @@ struct Prediction {
 
     // L2 stream (l2StreamModel 1; 0 otherwise).
     double l2HitBytes = 0.0;           // tile-load bytes served by the L2s, not HBM
+
+    // Power-limited clock (powerModel 1; 1.0 otherwise).
+    double powerClockFactor = 1.0;     // clock under this row's load over a pure MFMA stream's
 };
 
 }  // namespace ridge

@@ -43,6 +43,7 @@ typedef struct ridge_model_prediction {
     double reuseTilesM, reuseTilesN, compulsoryIntensity;
     double tailClockFactor;  /* clock of the last wave over the full-chip clock (clockModel 1) */
     double l2HitBytes;       /* tile-load bytes served by the L2s (l2StreamModel 1) */
+    double powerClockFactor; /* clock under this row's load over a pure MFMA stream's (powerModel 1) */
 } ridge_model_prediction_t;
 
 /* Default config (the reference's GemmConfig defaults, config.h:18-39). */

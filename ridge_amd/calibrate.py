@@ -23,7 +23,9 @@ MI355X differences from the reference driver:
     per-operand LDS rates feed ldsReadModel 1, and cal-hbm-bw's L2-resident read
     (l2HitBytesPerCycle) feeds l2StreamModel 1;
   * cal-smem-bw's ping-pong skeleton figures (reads under MFMAs, with and without
-    the GEMM's direct-to-LDS refill) are kept in the JSON as a record.
+    the GEMM's direct-to-LDS refill) are kept in the JSON as a record, and the ratio
+    of its clock with the refill to its clock with MFMAs alone is loadedClockRatio
+    (powerModel 1).
 """
 
 import argparse
@@ -108,6 +110,8 @@ def band_check(res, spec):
     ceiling = spec["clock_hz"] * 1.05 / res["clockHz"]
     for key in CLOCK_RATIO_KEYS:
         ok &= check(key, res[key], 0.98, ceiling, "x", "over the full-chip loaded clock")
+    ok &= check("loadedClockRatio", loaded_clock_ratio(res), 0.5, 1.0, "x",
+                "skeleton clock with reads and refill over MFMAs alone; data movement costs power")
     ok &= check("ldsAReadBytesPerCycle", res["ldsAReadBytesPerCycle"], 0.25 * res["ldsControlBytesPerCycle"],
                 1.05 * res["ldsControlBytesPerCycle"], "B/cycle/CU")
     ok &= check("ldsBTrReadBytesPerCycle", res["ldsBTrReadBytesPerCycle"], 0.125 * res["ldsControlBytesPerCycle"],
@@ -120,7 +124,14 @@ CLOCK_RATIO_KEYS = ["clockRatioHalfCus", "clockRatioQuarterCus", "clockRatioEigh
 # What the four benchmarks must report for a JSON to be written.
 REQUIRED_KEYS = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
                  "smemBytesPerCycle", "ldsControlBytesPerCycle", "ldsAReadBytesPerCycle", "ldsBTrReadBytesPerCycle",
-                 "hbmBytesPerSec", "l2HitBytesPerCycle", "warpsNeededToHide"] + CLOCK_RATIO_KEYS
+                 "hbmBytesPerSec", "l2HitBytesPerCycle", "warpsNeededToHide", "pingPongMfmaCyclesClockHz",
+                 "pingPongRefillStepCyclesClockHz"] + CLOCK_RATIO_KEYS
+
+
+def loaded_clock_ratio(res):
+    """The ping-pong skeleton's clock with the GEMM's operand reads and refill over
+    its clock with the MFMAs alone (cal-smem-bw): the model's powerModel 1."""
+    return res["pingPongRefillStepCyclesClockHz"] / res["pingPongMfmaCyclesClockHz"]
 
 # Figures of the ping-pong skeleton (cal-smem-bw), kept in the JSON as a record;
 # the model reads none of them.
@@ -171,6 +182,8 @@ def hardware_json(res, spec, arch):
         "clockModel": 1,
         "l2StreamModel": 1,
         "l2HitBytesPerCycle": res["l2HitBytesPerCycle"],
+        "powerModel": 1,
+        "loadedClockRatio": loaded_clock_ratio(res),
     }
     for key in CLOCK_RATIO_KEYS:
         out[key] = res[key]

@@ -230,6 +230,8 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
         !optionalNumber(kv, "clockRatioSixteenthCus", h.clockRatio[3], err) ||
         !optionalInteger(kv, "l2StreamModel", h.l2StreamModel, err) ||
         !optionalNumber(kv, "l2HitBytesPerCycle", h.l2HitBytesPerCycle, err) ||
+        !optionalInteger(kv, "powerModel", h.powerModel, err) ||
+        !optionalNumber(kv, "loadedClockRatio", h.loadedClockRatio, err) ||
         !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
         err = path + ": " + err;
         return false;
@@ -258,6 +260,10 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
     }
     if (h.l2StreamModel == 1 && h.l2HitBytesPerCycle <= 0.0) {
         err = path + ": l2StreamModel 1 needs a positive l2HitBytesPerCycle";
+        return false;
+    }
+    if (h.powerModel == 1 && (h.loadedClockRatio <= 0.0 || h.loadedClockRatio > 1.0)) {
+        err = path + ": powerModel 1 needs loadedClockRatio in (0, 1]";
         return false;
     }
     h.calibrated = true;

@@ -33,6 +33,9 @@
 //   last-wave clock       = hw.clockModel 1: a last wave that leaves CUs idle runs
 //                           at the calibrated power-limited clock for its busy
 //                           share of CUs (reference: one clock for every wave)
+//   power-limited clock   = hw.powerModel 1: the clock falls with the share of
+//                           time the matrix pipes are busy, to loadedClockRatio
+//                           when they always are (reference: one clock)
 //   L2 stream             = hw.l2StreamModel 1: tile loads the L2s serve take
 //                           their own time, in series with the HBM stream
 //                           (reference: the HBM roofline alone)
@@ -255,8 +258,16 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // Compute ceiling: resident workgroups share the matrix pipes, so occupancy
     // hides latency but never multiplies the peak.
     const double peakTensorTFLOPS = (double(mma.flops) / hw.mmaCyclesPerInst) * hw.clockHz * hw.numSMs / 1e12;
-    const double computeTFLOPS =
-        peakTensorTFLOPS * smEfficiency * occFactor * clockedWaveEfficiency * envelopeEfficiency;
+    double computeTFLOPS = peakTensorTFLOPS * smEfficiency * occFactor * clockedWaveEfficiency * envelopeEfficiency;
+    if (hw.powerModel == 1) {
+        // The chip is power-limited: with the GEMM's operand reads and refill under
+        // fully busy matrix pipes the clock falls to loadedClockRatio of a pure
+        // MFMA stream's; a row that keeps the pipes busy a share u of the time
+        // pays that share of the drop.
+        const double u = std::min(1.0, computeTFLOPS / peakTensorTFLOPS);
+        p.powerClockFactor = 1.0 - (1.0 - hw.loadedClockRatio) * u;
+        computeTFLOPS *= p.powerClockFactor;
+    }
     p.peakTensorTFLOPS = peakTensorTFLOPS;
     p.computeTFLOPS = computeTFLOPS;
 

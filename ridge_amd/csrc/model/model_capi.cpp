@@ -128,6 +128,7 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     out->compulsoryIntensity = p.compulsoryIntensity;
     out->tailClockFactor = p.tailClockFactor;
     out->l2HitBytes = p.l2HitBytes;
+    out->powerClockFactor = p.powerClockFactor;
     return 0;
 }
 

@@ -120,4 +120,4 @@ def test_binding_struct_layouts_match_the_libraries():
     assert L.ridge_model_config_size() == ctypes.sizeof(RM._Config)
     assert L.ridge_model_prediction_size() == ctypes.sizeof(RM._Prediction)
     # The prediction ends with the two gfx950 fields, after the reference's.
-    assert [f for f, _ in RM._Prediction._fields_][-2:] == ["tailClockFactor", "l2HitBytes"]
+    assert [f for f, _ in RM._Prediction._fields_][-3:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor"]

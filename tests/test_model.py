@@ -478,3 +478,28 @@ def test_l2_stream_model_adds_the_l2_served_tile_loads(tmp_path):
     bad.write_text(_CDNA4_JSON % ', "l2StreamModel": 1')
     with pytest.raises(ValueError, match="l2StreamModel 1"):
         RM.Hardware(str(bad))
+
+
+def test_power_model_derates_by_matrix_pipe_share(tmp_path):
+    """powerModel 1 with loadedClockRatio 0.8: a row whose compute ceiling is a
+    share u of the matrix-pipe peak runs at clock x (1 - 0.2 u). The headline
+    tile at 4096^3 on the placeholders: smEff 1 (ping-pong), occupancy 1, one
+    full wave, envelope e, so u = e and the ceiling becomes e x (1 - 0.2 e) x
+    peak. A ratio above 1 (data movement that raises the clock) is refused."""
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % ', "powerModel": 1, "loadedClockRatio": 0.8')
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % "")
+    cfg = dict(M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=4, regsPerThread=197)
+    p_on = RM.predict(RM.Hardware(str(on)), **cfg)
+    p_off = RM.predict(RM.Hardware(str(off)), **cfg)
+    u = p_off["computeTFLOPS"] / p_off["peakTensorTFLOPS"]
+    assert p_off["smEfficiency"] == 1.0 and p_off["waveEfficiency"] == 1.0
+    assert u == pytest.approx(p_off["envelopeEfficiency"] * p_off["occFactor"], rel=1e-12)
+    assert p_on["powerClockFactor"] == pytest.approx(1 - 0.2 * u, rel=1e-12)
+    assert p_on["computeTFLOPS"] == pytest.approx(p_off["computeTFLOPS"] * (1 - 0.2 * u), rel=1e-12)
+    assert p_off["powerClockFactor"] == 1.0
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "powerModel": 1, "loadedClockRatio": 1.2')
+    with pytest.raises(ValueError, match="powerModel 1"):
+        RM.Hardware(str(bad))
