@@ -73,6 +73,10 @@ struct HardwareModel {
                                      //    a shared panel) take their own time at
                                      //    l2HitBytesPerCycle x clockHz, in series with the HBM stream
     double l2HitBytesPerCycle = 0.0; // [CAL] whole GPU, per shader cycle, reads served by the XCDs' L2s
+    int uniformOverlapModel = 0;     // 0: a uniform-schedule K-step is reads + MFMAs (reference)
+                                     // 1: a workgroup of two waves per SIMD hides freeRunningOverlap
+                                     //    of the shorter phase under the longer
+    double freeRunningOverlap = 0.0; // [CAL] measured by cal-smem-bw's skeleton without barriers
     int powerModel = 0;              // 0: the loaded clock of a pure MFMA stream, clockHz (reference)
                                      // 1: a row that keeps the matrix pipes busy a share u of the
                                      //    time runs at clockHz x (1 - (1 - loadedClockRatio) u)

@@ -25,7 +25,8 @@ MI355X differences from the reference driver:
   * cal-smem-bw's ping-pong skeleton figures (reads under MFMAs, with and without
     the GEMM's direct-to-LDS refill) are kept in the JSON as a record, and the ratio
     of its clock with the refill to its clock with MFMAs alone is loadedClockRatio
-    (powerModel 1).
+    (powerModel 1); its free-running mode gives freeRunningOverlap
+    (uniformOverlapModel 1).
 """
 
 import argparse
@@ -110,6 +111,8 @@ def band_check(res, spec):
     ceiling = spec["clock_hz"] * 1.05 / res["clockHz"]
     for key in CLOCK_RATIO_KEYS:
         ok &= check(key, res[key], 0.98, ceiling, "x", "over the full-chip loaded clock")
+    ok &= check("freeRunningOverlap", res["freeRunningOverlap"], 0.0, 1.0, "",
+                "share of the shorter phase two free-running waves per SIMD hide")
     ok &= check("loadedClockRatio", loaded_clock_ratio(res), 0.5, 1.0, "x",
                 "skeleton clock with reads and refill over MFMAs alone; data movement costs power")
     ok &= check("ldsAReadBytesPerCycle", res["ldsAReadBytesPerCycle"], 0.25 * res["ldsControlBytesPerCycle"],
@@ -125,7 +128,7 @@ CLOCK_RATIO_KEYS = ["clockRatioHalfCus", "clockRatioQuarterCus", "clockRatioEigh
 REQUIRED_KEYS = ["mmaCyclesPerInst", "impliedPeakTflops", "impliedPeakTflopsNominalClock", "clockHz",
                  "smemBytesPerCycle", "ldsControlBytesPerCycle", "ldsAReadBytesPerCycle", "ldsBTrReadBytesPerCycle",
                  "hbmBytesPerSec", "l2HitBytesPerCycle", "warpsNeededToHide", "pingPongMfmaCyclesClockHz",
-                 "pingPongRefillStepCyclesClockHz"] + CLOCK_RATIO_KEYS
+                 "pingPongRefillStepCyclesClockHz", "freeRunningOverlap"] + CLOCK_RATIO_KEYS
 
 
 def loaded_clock_ratio(res):
@@ -182,6 +185,8 @@ def hardware_json(res, spec, arch):
         "clockModel": 1,
         "l2StreamModel": 1,
         "l2HitBytesPerCycle": res["l2HitBytesPerCycle"],
+        "uniformOverlapModel": 1,
+        "freeRunningOverlap": res["freeRunningOverlap"],
         "powerModel": 1,
         "loadedClockRatio": loaded_clock_ratio(res),
     }

@@ -230,6 +230,8 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
         !optionalNumber(kv, "clockRatioSixteenthCus", h.clockRatio[3], err) ||
         !optionalInteger(kv, "l2StreamModel", h.l2StreamModel, err) ||
         !optionalNumber(kv, "l2HitBytesPerCycle", h.l2HitBytesPerCycle, err) ||
+        !optionalInteger(kv, "uniformOverlapModel", h.uniformOverlapModel, err) ||
+        !optionalNumber(kv, "freeRunningOverlap", h.freeRunningOverlap, err) ||
         !optionalInteger(kv, "powerModel", h.powerModel, err) ||
         !optionalNumber(kv, "loadedClockRatio", h.loadedClockRatio, err) ||
         !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
@@ -260,6 +262,10 @@ bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, st
     }
     if (h.l2StreamModel == 1 && h.l2HitBytesPerCycle <= 0.0) {
         err = path + ": l2StreamModel 1 needs a positive l2HitBytesPerCycle";
+        return false;
+    }
+    if (h.uniformOverlapModel == 1 && (h.freeRunningOverlap < 0.0 || h.freeRunningOverlap > 1.0)) {
+        err = path + ": uniformOverlapModel 1 needs freeRunningOverlap in [0, 1]";
         return false;
     }
     if (h.powerModel == 1 && (h.loadedClockRatio <= 0.0 || h.loadedClockRatio > 1.0)) {

@@ -33,6 +33,9 @@
 //   last-wave clock       = hw.clockModel 1: a last wave that leaves CUs idle runs
 //                           at the calibrated power-limited clock for its busy
 //                           share of CUs (reference: one clock for every wave)
+//   uniform overlap       = hw.uniformOverlapModel 1: an 8-wave uniform workgroup
+//                           (two waves per SIMD) hides the measured share of the
+//                           shorter phase under the longer (reference: in series)
 //   power-limited clock   = hw.powerModel 1: the clock falls with the share of
 //                           time the matrix pipes are busy, to loadedClockRatio
 //                           when they always are (reference: one clock)
@@ -170,7 +173,13 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // costs the longer of the two instead of their sum.
     const bool derivedPingPong = hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM && cfg.stages >= 3;
     const bool pingPong = hw.pingPongModel == 1 && (cfg.schedule < 0 ? derivedPingPong : cfg.schedule == 1);
-    const double tStep = pingPong ? std::max(tCompute, tSmem) : tCompute + tSmem;
+    double tStep = pingPong ? std::max(tCompute, tSmem) : tCompute + tSmem;
+    // uniformOverlapModel 1: the two waves per SIMD of an 8-wave uniform workgroup
+    // hide part of the shorter phase under the longer with no schedule doing it:
+    // the share cal-smem-bw measures for the same waves without barriers.
+    if (!pingPong && hw.uniformOverlapModel == 1 && !persistent && hw.simdsPerSM > 0 &&
+        numWarps == 2 * hw.simdsPerSM)
+        tStep -= hw.freeRunningOverlap * std::min(tCompute, tSmem);
     const double smEfficiency = tCompute / tStep;
     p.tComputeCycles = tCompute;
     p.tSmemCycles = tSmem;

@@ -503,3 +503,27 @@ def test_power_model_derates_by_matrix_pipe_share(tmp_path):
     bad.write_text(_CDNA4_JSON % ', "powerModel": 1, "loadedClockRatio": 1.2')
     with pytest.raises(ValueError, match="powerModel 1"):
         RM.Hardware(str(bad))
+
+
+def test_uniform_overlap_model_hides_part_of_the_shorter_phase(tmp_path):
+    """uniformOverlapModel 1 with freeRunningOverlap 0.75 on the placeholders
+    (4 cycles per MFMA per CU, 128 B/cycle LDS): the 8-wave uniform 256x256x32
+    w128x64 tile at 2 stages has tC = 1024, tS = 768 and runs
+    1024 + 768 - 0.75 x 768 = 1216 cycles per K-step (in series: 1792). A 4-wave
+    uniform workgroup (one wave per SIMD) and the ping-pong rows are unchanged."""
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % ', "uniformOverlapModel": 1, "freeRunningOverlap": 0.75')
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % "")
+    hw_on, hw_off = RM.Hardware(str(on)), RM.Hardware(str(off))
+    eight = dict(M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=2, regsPerThread=197)
+    assert RM.predict(hw_off, **eight)["tStepCycles"] == pytest.approx(1792.0)
+    assert RM.predict(hw_on, **eight)["tStepCycles"] == pytest.approx(1216.0)
+    four = dict(eight, BN=128)
+    assert RM.predict(hw_on, **four)["tStepCycles"] == RM.predict(hw_off, **four)["tStepCycles"]
+    pp = dict(eight, stages=4)
+    assert RM.predict(hw_on, **pp)["tStepCycles"] == pytest.approx(1024.0)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "uniformOverlapModel": 1, "freeRunningOverlap": 1.5')
+    with pytest.raises(ValueError, match="uniformOverlapModel 1"):
+        RM.Hardware(str(bad))
