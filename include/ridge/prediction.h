@@ -18,11 +18,11 @@ struct Prediction {
     double predictedTFLOPS = 0.0;
     Bottleneck bottleneck = Bottleneck::TensorCore;
 
-    double computeTFLOPS = 0.0;        // compute ceiling after all deratings
-    double hbmTFLOPS = 0.0;            // HBM roofline ceiling
-    double peakTensorTFLOPS = 0.0;     // matrix-pipe peak, no derating
-    double smEfficiency = 0.0;         // tCompute / tStep
-    double occFactor = 0.0;            // latency hiding, 1.0 = fully hidden
+    double computeTFLOPS = 0.0;        // matrix peak x read, latency, grid and fill/drain factors
+    double hbmTFLOPS = 0.0;            // DRAM bandwidth x arithmetic intensity
+    double peakTensorTFLOPS = 0.0;     // MFMA issue rate x CUs x clock, nothing subtracted
+    double smEfficiency = 0.0;         // share of a K-step the matrix pipe is issuing
+    double occFactor = 0.0;            // resident waves over those needed, capped at 1
     double arithmeticIntensity = 0.0;  // FLOP per DRAM byte, after cache reuse
     double baseIntensity = 0.0;        // FLOP per byte of one tile, before reuse
     double l2ReuseFactor = 0.0;        // arithmeticIntensity / baseIntensity
@@ -42,7 +42,7 @@ struct Prediction {
     int ctasPerSM = 0;                 // resident workgroups per CU (SM)
     double tComputeCycles = 0.0;
     double tSmemCycles = 0.0;
-    double tStepCycles = 0.0;          // tCompute + tSmem, in series
+    double tStepCycles = 0.0;          // cycles of one K-step, both phases counted
 
     // CDNA4 reuse terms (zero in the reference's square-reuse mode).
     double reuseTilesM = 0.0;          // resident row tiles sharing one XCD's L2

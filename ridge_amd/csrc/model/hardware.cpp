@@ -1,13 +1,15 @@
 // hardware.cpp -- built-in hardware models and the flat-JSON loader.
-// Counterpart of the reference's src/hardware.cpp (a100 :19-34, loader :149-200).
+// Counterpart of the reference's src/hardware.cpp (a100 :19-34, loader :149-200):
+// the same all-or-nothing contract and required keys, read through the build's
+// shared text reader (common/textio.hpp) and a declarative key schema.
 
 #include "ridge/hardware.h"
 
-#include <cctype>
-#include <cstdlib>
-#include <fstream>
-#include <map>
-#include <sstream>
+#include "../common/textio.hpp"
+
+#include <cstdint>
+#include <string>
+#include <vector>
 
 namespace ridge {
 
@@ -72,204 +74,119 @@ HardwareModel HardwareModel::mi355x() {
 
 namespace {
 
-// Parser for one flat JSON object of string and number values. The "note" field
-// holds prose that can mention key names, so values are read by parsing, never by
-// searching for substrings.
-class FlatJson {
-public:
-    explicit FlatJson(const std::string& text) : s_(text) {}
-
-    bool parse(std::map<std::string, std::string>& out, std::string& err) {
-        ws();
-        if (!eat('{', err)) return false;
-        ws();
-        if (peek() == '}') return true;
-        while (true) {
-            ws();
-            std::string key, value;
-            if (!str(key, err)) return false;
-            ws();
-            if (!eat(':', err)) return false;
-            ws();
-            if (peek() == '"') {
-                if (!str(value, err)) return false;
-            } else if (!bare(value, err)) {
-                return false;
-            }
-            out[key] = value;
-            ws();
-            if (peek() == ',') {
-                ++i_;
-                continue;
-            }
-            if (peek() == '}') return true;
-            err = "expected ',' or '}' at offset " + std::to_string(i_);
-            return false;
-        }
-    }
-
-private:
-    char peek() const { return i_ < s_.size() ? s_[i_] : '\0'; }
-    void ws() {
-        while (i_ < s_.size() && std::isspace((unsigned char)s_[i_])) ++i_;
-    }
-    bool eat(char c, std::string& err) {
-        if (peek() != c) {
-            err = std::string("expected '") + c + "' at offset " + std::to_string(i_);
-            return false;
-        }
-        ++i_;
-        return true;
-    }
-    bool str(std::string& out, std::string& err) {
-        if (!eat('"', err)) return false;
-        out.clear();
-        while (i_ < s_.size() && s_[i_] != '"') {
-            if (s_[i_] == '\\' && i_ + 1 < s_.size()) ++i_;
-            out.push_back(s_[i_++]);
-        }
-        return eat('"', err);
-    }
-    bool bare(std::string& out, std::string& err) {
-        const size_t b = i_;
-        while (i_ < s_.size() && s_[i_] != ',' && s_[i_] != '}' && !std::isspace((unsigned char)s_[i_])) ++i_;
-        if (i_ == b) {
-            err = "empty value at offset " + std::to_string(b);
-            return false;
-        }
-        out = s_.substr(b, i_ - b);
-        return true;
-    }
-
-    const std::string& s_;
-    size_t i_ = 0;
+// How one JSON key lands in a HardwareModel field. A required key must be
+// present; a key marked `positive` must also be > 0 (a zero there would divide
+// by zero or silently zero a ceiling). Keys the schema does not name (the
+// calibration record: skeleton cycles, curves, the note) are ignored.
+struct KeyRule {
+    const char* key;
+    bool required;
+    bool positive;
+    double* real;  // exactly one of real / integer is set
+    int* integer;
 };
 
-bool number(const std::map<std::string, std::string>& kv, const char* key, double& out, std::string& err) {
-    auto it = kv.find(key);
-    if (it == kv.end()) {
-        err = std::string("missing required key \"") + key + "\"";
-        return false;
+std::vector<KeyRule> schemaFor(HardwareModel& h) {
+    auto R = [](const char* k, double& f, bool req = false, bool pos = false) { return KeyRule{k, req, pos, &f, nullptr}; };
+    auto I = [](const char* k, int& f, bool req = false, bool pos = false) { return KeyRule{k, req, pos, nullptr, &f}; };
+    return {
+        // The ten constants every hardware description carries (the
+        // reference's required set); clock and the [CAL] rates must be positive.
+        I("numSMs", h.numSMs, true, true), R("clockHz", h.clockHz, true, true),
+        R("mmaCyclesPerInst", h.mmaCyclesPerInst, true, true), R("smemBytesPerCycle", h.smemBytesPerCycle, true, true),
+        R("hbmBytesPerSec", h.hbmBytesPerSec, true, true), I("regsPerSM", h.regsPerSM, true),
+        I("smemBytesPerSM", h.smemBytesPerSM, true), I("maxWarpsPerSM", h.maxWarpsPerSM, true),
+        I("maxCtasPerSM", h.maxCtasPerSM, true), R("warpsNeededToHide", h.warpsNeededToHide, true, true),
+        // Target description (defaults: the arch's built-in model).
+        I("waveSize", h.waveSize), I("mmaM", h.mmaM), I("mmaN", h.mmaN), I("mmaK", h.mmaK),
+        I("simdsPerSM", h.simdsPerSM), I("regsPerSimdLane", h.regsPerSimdLane), I("regGranule", h.regGranule),
+        I("numXcds", h.numXcds), I("cBytes", h.cBytes),
+        // Model terms and the constants they read.
+        I("l2ReuseModel", h.l2ReuseModel), I("prologueModel", h.prologueModel), I("pingPongModel", h.pingPongModel),
+        I("persistentModel", h.persistentModel), I("ldsReadModel", h.ldsReadModel),
+        R("ldsAReadBytesPerCycle", h.ldsAReadBytesPerCycle), R("ldsBTrReadBytesPerCycle", h.ldsBTrReadBytesPerCycle),
+        I("clockModel", h.clockModel), R("clockRatioHalfCus", h.clockRatio[0]),
+        R("clockRatioQuarterCus", h.clockRatio[1]), R("clockRatioEighthCus", h.clockRatio[2]),
+        R("clockRatioSixteenthCus", h.clockRatio[3]), I("l2StreamModel", h.l2StreamModel),
+        R("l2HitBytesPerCycle", h.l2HitBytesPerCycle), I("uniformOverlapModel", h.uniformOverlapModel),
+        R("freeRunningOverlap", h.freeRunningOverlap), I("powerModel", h.powerModel),
+        R("loadedClockRatio", h.loadedClockRatio), R("warpsNeededToHideIlp8", h.warpsNeededToHideIlp8),
+    };
+}
+
+ridgeio::Status applySchema(const ridgeio::FlatObject& kv, const std::vector<KeyRule>& schema) {
+    for (const KeyRule& rule : schema) {
+        const auto it = kv.find(rule.key);
+        const std::string name = std::string("\"") + rule.key + "\"";
+        if (it == kv.end()) {
+            if (rule.required) return ridgeio::Status::failure("", "required constant " + name + " is absent");
+            continue;
+        }
+        double value = 0.0;
+        if (rule.integer) {
+            long long n = 0;
+            if (!ridgeio::toInteger(it->second, n) || n < INT32_MIN || n > INT32_MAX)
+                return ridgeio::Status::failure("", name + " must be an integer, found " + it->second);
+            *rule.integer = static_cast<int>(n);
+            value = double(n);
+        } else {
+            if (!ridgeio::toReal(it->second, value))
+                return ridgeio::Status::failure("", name + " must be a number, found " + it->second);
+            *rule.real = value;
+        }
+        if (rule.positive && !(value > 0.0))
+            return ridgeio::Status::failure("", name + " must be positive, found " + it->second);
     }
-    char* end = nullptr;
-    const double v = std::strtod(it->second.c_str(), &end);
-    if (end == it->second.c_str() || *end != '\0') {
-        err = std::string("key \"") + key + "\" is not a number: " + it->second;
-        return false;
-    }
-    out = v;
-    return true;
+    return ridgeio::Status();
 }
 
-bool integer(const std::map<std::string, std::string>& kv, const char* key, int& out, std::string& err) {
-    double d = 0.0;
-    if (!number(kv, key, d, err)) return false;
-    out = static_cast<int>(d);
-    return true;
-}
-
-bool optionalInteger(const std::map<std::string, std::string>& kv, const char* key, int& out, std::string& err) {
-    if (kv.find(key) == kv.end()) return true;
-    return integer(kv, key, out, err);
-}
-
-bool optionalNumber(const std::map<std::string, std::string>& kv, const char* key, double& out, std::string& err) {
-    if (kv.find(key) == kv.end()) return true;
-    return number(kv, key, out, err);
+// Consistency of a loaded model: target-description values in range and every
+// switched-on term given the constants it reads. Empty when consistent.
+std::string inconsistency(const HardwareModel& h) {
+    if (h.waveSize <= 0 || h.mmaM <= 0 || h.mmaN <= 0 || h.mmaK <= 0 || h.regGranule <= 0 || h.numXcds <= 0 ||
+        h.cBytes <= 0 || h.simdsPerSM < 0 || (h.simdsPerSM > 0 && h.regsPerSimdLane <= 0))
+        return "the target description (waveSize, mma shape, register files, XCDs, cBytes) is out of range";
+    if (h.ldsReadModel == 1 && !(h.ldsAReadBytesPerCycle > 0.0 && h.ldsBTrReadBytesPerCycle > 0.0))
+        return "ldsReadModel 1 reads ldsAReadBytesPerCycle and ldsBTrReadBytesPerCycle, which must be positive";
+    if (h.clockModel == 1 &&
+        !(h.clockRatio[0] > 0.0 && h.clockRatio[1] > 0.0 && h.clockRatio[2] > 0.0 && h.clockRatio[3] > 0.0))
+        return "clockModel 1 reads the four clockRatio* constants, which must be positive";
+    if (h.l2StreamModel == 1 && !(h.l2HitBytesPerCycle > 0.0))
+        return "l2StreamModel 1 reads l2HitBytesPerCycle, which must be positive";
+    if (h.uniformOverlapModel == 1 && !(h.freeRunningOverlap >= 0.0 && h.freeRunningOverlap <= 1.0))
+        return "uniformOverlapModel 1 reads freeRunningOverlap, which must lie in [0, 1]";
+    if (h.powerModel == 1 && !(h.loadedClockRatio > 0.0 && h.loadedClockRatio <= 1.0))
+        return "powerModel 1 reads loadedClockRatio, which must lie in (0, 1]";
+    return "";
 }
 
 }  // namespace
 
 bool HardwareModel::loadFromJson(const std::string& path, HardwareModel& out, std::string& err) {
-    std::ifstream in(path);
-    if (!in) {
-        err = "cannot open " + path;
+    std::string text;
+    ridgeio::FlatObject kv;
+    ridgeio::Status st = ridgeio::readWholeFile(path, text);
+    if (st.ok()) st = ridgeio::parseFlatObject(text, path, kv);
+    if (!st.ok()) {
+        err = st.message();
         return false;
     }
-    std::ostringstream ss;
-    ss << in.rdbuf();
-    const std::string text = ss.str();
-    std::map<std::string, std::string> kv;
-    FlatJson parser(text);
-    if (!parser.parse(kv, err)) {
-        err = path + ": " + err;
-        return false;
-    }
-
-    // Built in a temporary so a failure cannot leave a half-calibrated model.
-    auto archIt = kv.find("arch");
-    HardwareModel h = (archIt != kv.end() && archIt->second == "gfx950") ? mi355x() : HardwareModel();
-    auto name = kv.find("name");
+    // "arch": "gfx950" starts from the CDNA4 target description; anything else
+    // from the reference's sm_80 defaults. The result is assembled in a local
+    // and only copied out once complete, so a failure leaves `out` untouched.
+    const auto arch = kv.find("arch");
+    HardwareModel h = (arch != kv.end() && arch->second == "gfx950") ? mi355x() : HardwareModel();
+    const auto name = kv.find("name");
     h.name = name != kv.end() ? name->second : path;
-
-    if (!integer(kv, "numSMs", h.numSMs, err) || !number(kv, "clockHz", h.clockHz, err) ||
-        !number(kv, "mmaCyclesPerInst", h.mmaCyclesPerInst, err) ||
-        !number(kv, "smemBytesPerCycle", h.smemBytesPerCycle, err) ||
-        !number(kv, "hbmBytesPerSec", h.hbmBytesPerSec, err) || !integer(kv, "regsPerSM", h.regsPerSM, err) ||
-        !integer(kv, "smemBytesPerSM", h.smemBytesPerSM, err) ||
-        !integer(kv, "maxWarpsPerSM", h.maxWarpsPerSM, err) ||
-        !integer(kv, "maxCtasPerSM", h.maxCtasPerSM, err) ||
-        !number(kv, "warpsNeededToHide", h.warpsNeededToHide, err) ||
-        !optionalInteger(kv, "waveSize", h.waveSize, err) || !optionalInteger(kv, "mmaM", h.mmaM, err) ||
-        !optionalInteger(kv, "mmaN", h.mmaN, err) || !optionalInteger(kv, "mmaK", h.mmaK, err) ||
-        !optionalInteger(kv, "simdsPerSM", h.simdsPerSM, err) ||
-        !optionalInteger(kv, "regsPerSimdLane", h.regsPerSimdLane, err) ||
-        !optionalInteger(kv, "regGranule", h.regGranule, err) ||
-        !optionalInteger(kv, "numXcds", h.numXcds, err) || !optionalInteger(kv, "cBytes", h.cBytes, err) ||
-        !optionalInteger(kv, "l2ReuseModel", h.l2ReuseModel, err) ||
-        !optionalInteger(kv, "prologueModel", h.prologueModel, err) ||
-        !optionalInteger(kv, "pingPongModel", h.pingPongModel, err) ||
-        !optionalInteger(kv, "persistentModel", h.persistentModel, err) ||
-        !optionalInteger(kv, "ldsReadModel", h.ldsReadModel, err) ||
-        !optionalNumber(kv, "ldsAReadBytesPerCycle", h.ldsAReadBytesPerCycle, err) ||
-        !optionalNumber(kv, "ldsBTrReadBytesPerCycle", h.ldsBTrReadBytesPerCycle, err) ||
-        !optionalInteger(kv, "clockModel", h.clockModel, err) ||
-        !optionalNumber(kv, "clockRatioHalfCus", h.clockRatio[0], err) ||
-        !optionalNumber(kv, "clockRatioQuarterCus", h.clockRatio[1], err) ||
-        !optionalNumber(kv, "clockRatioEighthCus", h.clockRatio[2], err) ||
-        !optionalNumber(kv, "clockRatioSixteenthCus", h.clockRatio[3], err) ||
-        !optionalInteger(kv, "l2StreamModel", h.l2StreamModel, err) ||
-        !optionalNumber(kv, "l2HitBytesPerCycle", h.l2HitBytesPerCycle, err) ||
-        !optionalInteger(kv, "uniformOverlapModel", h.uniformOverlapModel, err) ||
-        !optionalNumber(kv, "freeRunningOverlap", h.freeRunningOverlap, err) ||
-        !optionalInteger(kv, "powerModel", h.powerModel, err) ||
-        !optionalNumber(kv, "loadedClockRatio", h.loadedClockRatio, err) ||
-        !optionalNumber(kv, "warpsNeededToHideIlp8", h.warpsNeededToHideIlp8, err)) {
-        err = path + ": " + err;
+    if (arch != kv.end()) h.arch = arch->second;
+    st = applySchema(kv, schemaFor(h));
+    if (!st.ok()) {
+        err = path + ": " + st.message();
         return false;
     }
-    if (archIt != kv.end()) h.arch = archIt->second;
-
-    // Zeros would divide by zero or silently zero a ceiling (reference :190-195).
-    if (h.numSMs <= 0 || h.clockHz <= 0.0 || h.mmaCyclesPerInst <= 0.0 || h.smemBytesPerCycle <= 0.0 ||
-        h.hbmBytesPerSec <= 0.0 || h.warpsNeededToHide <= 0.0) {
-        err = path + ": a required constant is zero or negative";
-        return false;
-    }
-    if (h.waveSize <= 0 || h.mmaM <= 0 || h.mmaN <= 0 || h.mmaK <= 0 || h.regGranule <= 0 || h.numXcds <= 0 ||
-        h.cBytes <= 0 || h.simdsPerSM < 0 || (h.simdsPerSM > 0 && h.regsPerSimdLane <= 0)) {
-        err = path + ": a target-description key is out of range";
-        return false;
-    }
-    if (h.ldsReadModel == 1 && (h.ldsAReadBytesPerCycle <= 0.0 || h.ldsBTrReadBytesPerCycle <= 0.0)) {
-        err = path + ": ldsReadModel 1 needs positive ldsAReadBytesPerCycle and ldsBTrReadBytesPerCycle";
-        return false;
-    }
-    if (h.clockModel == 1 &&
-        (h.clockRatio[0] <= 0.0 || h.clockRatio[1] <= 0.0 || h.clockRatio[2] <= 0.0 || h.clockRatio[3] <= 0.0)) {
-        err = path + ": clockModel 1 needs the four positive clockRatio* keys";
-        return false;
-    }
-    if (h.l2StreamModel == 1 && h.l2HitBytesPerCycle <= 0.0) {
-        err = path + ": l2StreamModel 1 needs a positive l2HitBytesPerCycle";
-        return false;
-    }
-    if (h.uniformOverlapModel == 1 && (h.freeRunningOverlap < 0.0 || h.freeRunningOverlap > 1.0)) {
-        err = path + ": uniformOverlapModel 1 needs freeRunningOverlap in [0, 1]";
-        return false;
-    }
-    if (h.powerModel == 1 && (h.loadedClockRatio <= 0.0 || h.loadedClockRatio > 1.0)) {
-        err = path + ": powerModel 1 needs loadedClockRatio in (0, 1]";
+    const std::string bad = inconsistency(h);
+    if (!bad.empty()) {
+        err = path + ": " + bad;
         return false;
     }
     h.calibrated = true;

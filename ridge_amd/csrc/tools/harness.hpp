@@ -6,6 +6,8 @@
 
 #include "ridge_gemm.h"
 
+#include "../common/stats.hpp"
+
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -108,12 +110,8 @@ inline Timing timeTflops(const std::function<void()>& body, double flops, double
     return t;
 }
 
-inline double median(std::vector<double> v) {
-    if (v.empty()) return 0.0;
-    std::sort(v.begin(), v.end());
-    const size_t n = v.size();
-    return (n % 2) ? v[n / 2] : 0.5 * (v[n / 2 - 1] + v[n / 2]);
-}
+using ridgestat::dispersion;
+using ridgestat::middle;
 
 // hipBLASLt comparator over the C ABI, prepared once per shape.
 struct BlasLt {

@@ -31,6 +31,7 @@ import statistics
 import sys
 
 from ridge_amd import model as RM
+from ridge_amd import tables as T
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # The calibration the registration was made under (a frozen copy of
@@ -73,8 +74,7 @@ CONTROL_SIMD_UTIL_PCT = (80.0, 105.0)
 
 
 def _read_rows(path):
-    with open(path) as f:
-        return list(csv.DictReader(line for line in f if not line.startswith("#")))
+    return T.read(path).records
 
 
 def predict_row(hw, r):

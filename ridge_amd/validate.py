@@ -1,145 +1,190 @@
-"""Joins a measured sweep with model predictions and reports accuracy and ranking
-separately: a model can be good at one and bad at the other.
+"""Accuracy report: the model's predictions against a measured sweep.
 
     python -m ridge_amd.validate [--measured data/measured/mi355x.csv]
                                  [--registered data/sweep/mi355x-registered.csv]
                                  [--hw data/hardware/mi355x.json]
 
-Restates the reference's bench/validate.py:36-359: MAPE with its distribution,
-tie-averaged Spearman per shape, rank-of-best and regret@1 as [pessimistic,
-optimistic] ranges over predicted ties, the predicted label distribution, and
-the gate that the measured set is exactly the registered cross product of
-shapes x kernel table. The kernel table comes from the C ABI
-(ridge_gemm_variant_table_csv) instead of a regex over a source file. Statistics
-are written out, not imported; predictions come from `ridge-predict --batch`.
-Exit code 1 when a gate fails (MAPE ceiling, cross-product mismatch).
+Counterpart of the reference's bench/validate.py:36-359, with the same report
+contents: absolute error (MAPE, median, p90, max, mean signed error), ranking
+quality per shape (Spearman's rho on mid-ranks, the predicted position of the
+measured-best config and the regret of the predicted top pick, both as ranges
+over predicted ties, since a tie is not a decision the model made), the
+predicted label distribution, and the integrity gate that the measured rows are
+exactly the registered shapes x the kernel table. Here the table is read from
+the C ABI (ridge_gemm_variant_table_csv), and the report adds the error by
+resident wavefronts per SIMD and schedule. Predictions come from
+`ridge-predict --batch`; statistics are in ridge_amd.stats, tables are read by
+ridge_amd.tables. Exit code 1 when a gate fails.
 """
 
 import argparse
 import collections
-import csv
 import os
 import sys
 import tempfile
+from dataclasses import dataclass
 
 from ridge_amd import model as RM
+from ridge_amd import stats as S
+from ridge_amd import tables as T
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KEY_COLUMNS = ("BM", "BN", "BK", "WM", "WN", "stages", "groupM")
+SCHEDULES = {"0": "uniform", "1": "ping-pong", "2": "persistent"}
 
 
-def average_ranks(xs):
-    """1-based ranks with ties averaged (what Spearman requires)."""
-    order = sorted(range(len(xs)), key=lambda i: xs[i])
-    ranks = [0.0] * len(xs)
-    i = 0
-    while i < len(order):
-        j = i
-        while j + 1 < len(order) and xs[order[j + 1]] == xs[order[i]]:
-            j += 1
-        avg = (i + j) / 2.0 + 1.0
-        for k in range(i, j + 1):
-            ranks[order[k]] = avg
-        i = j + 1
-    return ranks
-
-
-def pearson(a, b):
-    n = len(a)
-    if n < 2:
-        return float("nan")
-    ma, mb = sum(a) / n, sum(b) / n
-    num = sum((x - ma) * (y - mb) for x, y in zip(a, b))
-    da = sum((x - ma) ** 2 for x in a) ** 0.5
-    db = sum((y - mb) ** 2 for y in b) ** 0.5
-    if da == 0.0 or db == 0.0:
-        return float("nan")  # no variance on one side: a result, not an accident
-    return num / (da * db)
-
-
-def spearman(a, b):
-    return pearson(average_ranks(a), average_ranks(b))
-
-
-def percentile(xs, p):
-    if not xs:
-        return float("nan")
-    s = sorted(xs)
-    if len(s) == 1:
-        return s[0]
-    idx = (len(s) - 1) * p / 100.0
-    lo, hi = int(idx), min(int(idx) + 1, len(s) - 1)
-    return s[lo] + (s[hi] - s[lo]) * (idx - lo)
-
-
-def rank_bounds(rows, key_pred="pred_tflops", key_meas="tflops"):
-    """(best, worst) rank of the measured-best config in the predicted order."""
-    best = max(rows, key=lambda r: float(r[key_meas]))
-    p = float(best[key_pred])
-    better = sum(1 for r in rows if float(r[key_pred]) > p)
-    tied = sum(1 for r in rows if float(r[key_pred]) == p)
-    return better + 1, better + tied
-
-
-def regret_bounds(rows, key_pred="pred_tflops", key_meas="tflops"):
-    """(worst, best, tie size) fraction lost by taking the predicted top pick."""
-    measured_best = max(float(r[key_meas]) for r in rows)
-    top = max(float(r[key_pred]) for r in rows)
-    tied = [float(r[key_meas]) for r in rows if float(r[key_pred]) == top]
-    return (measured_best - min(tied)) / measured_best, (measured_best - max(tied)) / measured_best, len(tied)
-
-
-def load_registered(path):
-    shapes = []
-    for line in open(path):
-        line = line.strip()
-        if not line or line.startswith("#"):
-            continue
-        p = line.split(",")
-        shapes.append((int(p[0]), int(p[1]), int(p[2])))
-    return shapes
-
-
-def load_variant_table():
+def kernel_table_keys():
+    """The 7-field key of every row of the built kernel table, in table order."""
     from ridge_amd import gemm as G
-    rows = list(csv.DictReader(G.variant_table_csv().splitlines()))
-    return [tuple(int(r[k]) for k in ("BM", "BN", "BK", "WM", "WN", "stages", "groupM")) for r in rows]
+    table = T.parse(G.variant_table_csv().splitlines(), "ridge_gemm_variant_table_csv()", require=KEY_COLUMNS)
+    return [tuple(table.number(i, c, int) for c in KEY_COLUMNS) for i in range(len(table))]
 
 
-def cross_product_gate(rows, registered, variants):
-    expected = {(M, N, K) + v for (M, N, K) in registered for v in variants}
-    got = {tuple(int(r[k]) for k in ("M", "N", "K", "BM", "BN", "BK", "WM", "WN", "stages", "groupM"))
-           for r in rows}
-    return expected - got, got - expected
+def registered_gate(records, shapes, keys):
+    """(absent, unexpected): registered (shape + key) rows that were not measured,
+    and measured rows that were not registered."""
+    want = {(M, N, K) + key for (M, N, K, _tag) in shapes for key in keys}
+    have = {tuple(int(r[c]) for c in ("M", "N", "K") + KEY_COLUMNS) for r in records}
+    return want - have, have - want
 
 
-def read_meta(path):
-    meta = {}
-    for line in open(path):
-        if line.startswith("#"):
-            parts = line[1:].strip().split(",", 1)
-            if len(parts) == 2:
-                meta[parts[0].strip()] = parts[1].strip()
-    return meta
+@dataclass
+class Joined:
+    """One measured row with the model's prediction for it."""
+    record: dict
+    measured: float
+    predicted: float
+
+    @property
+    def signed_pct(self):
+        return (self.predicted - self.measured) / self.measured * 100.0
+
+    @property
+    def abs_pct(self):
+        return abs(self.signed_pct)
 
 
-SCHEDULE_NAMES = {"0": "uniform", "1": "ping-pong", "2": "persistent"}
+def join(measured_path, hw):
+    with tempfile.TemporaryDirectory() as td:
+        out = os.path.join(td, "pred.csv")
+        sys.stderr.write(RM.predict_batch(measured_path, out, hw=hw))
+        table = T.read(out, require=("M", "N", "K", "tflops", "pred_tflops", "pred_bottleneck") + KEY_COLUMNS)
+    return [Joined(r, table.number(i, "tflops"), table.number(i, "pred_tflops")) for i, r in enumerate(table)]
 
 
 def error_by_resident_waves(rows, simds_per_cu=4):
-    """MAPE and mean signed error per (resident wavefronts per SIMD, schedule)
-    class: workgroups resident per CU (the model's ctasPerSM) x wavefronts per
-    workgroup / SIMDs per CU. Needs the pred_ctas_per_sm column and a per-row
-    schedule; returns {} for CSVs without them (the reference's A100 sweep)."""
-    if not rows or "pred_ctas_per_sm" not in rows[0] or "schedule" not in rows[0]:
+    """{(waves per SIMD, workgroup kind): (rows, MAPE %, mean signed %)}. A row's
+    resident wavefronts per SIMD are its predicted workgroups per CU times its
+    wavefronts per workgroup over the SIMDs of a CU. Empty for tables without
+    the pred_ctas_per_sm and schedule columns (the reference's A100 sweep)."""
+    if not rows or not {"pred_ctas_per_sm", "schedule"} <= set(rows[0].record):
         return {}
-    acc = {}
-    for r in rows:
+    groups = collections.defaultdict(list)
+    for j in rows:
+        r = j.record
         waves = (int(r["BM"]) // int(r["WM"])) * (int(r["BN"]) // int(r["WN"]))
         per_simd = int(float(r["pred_ctas_per_sm"])) * waves / simds_per_cu
-        key = (per_simd, "%d-wave %s" % (waves, SCHEDULE_NAMES.get(r["schedule"], r["schedule"])))
-        n, a, sg = acc.get(key, (0, 0.0, 0.0))
-        acc[key] = (n + 1, a + r["_abs"], sg + r["_signed"])
-    return {k: (n, a / n, sg / n) for k, (n, a, sg) in acc.items()}
+        kind = "%d-wave %s" % (waves, SCHEDULES.get(r["schedule"], r["schedule"]))
+        groups[(per_simd, kind)].append(j)
+    return {key: (len(js), sum(j.abs_pct for j in js) / len(js), sum(j.signed_pct for j in js) / len(js))
+            for key, js in groups.items()}
+
+
+@dataclass
+class ShapeRanking:
+    tag: str
+    rho: float
+    largest_tie: int
+    best_rank: tuple       # (optimistic, pessimistic)
+    regret1: tuple         # (pessimistic, optimistic), fractions
+    top_tie: int
+
+
+def rank_shapes(rows):
+    """One ShapeRanking per shape, in first-seen order."""
+    shapes = collections.OrderedDict()
+    for j in rows:
+        r = j.record
+        shapes.setdefault(r.get("tag") or "%sx%sx%s" % (r["M"], r["N"], r["K"]), []).append(j)
+    out = []
+    for tag, js in shapes.items():
+        meas = [j.measured for j in js]
+        pred = [j.predicted for j in js]
+        tie = S.top_tie(pred, meas)
+        best = max(meas)
+        out.append(ShapeRanking(tag, S.spearman(meas, pred),
+                                max(collections.Counter(pred).values()), S.best_rank_range(pred, meas),
+                                (S.regret(best, min(tie)), S.regret(best, max(tie))), len(tie)))
+    return out
+
+
+def _mean(xs):
+    return sum(xs) / len(xs) if xs else S.NAN
+
+
+def report(rows, meta, hw, gate_lines, mape_target, mape_ceiling):
+    """Prints the report; returns the list of failed gates."""
+    failed = []
+    rule = "-" * 74
+    print(rule)
+    print("ridge cost model against measurement")
+    print(rule)
+    for k in ("gpu", "cus", "sms", "nominal_clock_mhz", "warmup_seconds", "canary_drift_fraction"):
+        if k in meta:
+            print("  %-24s %s" % (k, meta[k]))
+    print("  %-24s %s\n" % ("hardware model", hw))
+    for line in gate_lines:
+        print(line)
+
+    errs = [j.abs_pct for j in rows]
+    mape = _mean(errs)
+    print("absolute error (%d rows)" % len(rows))
+    print("  %-22s %8.2f %%   (target <= %.0f%%, ceiling %.0f%%)" % ("MAPE", mape, mape_target, mape_ceiling))
+    for name, pct in (("median", 50), ("p90", 90)):
+        print("  %-22s %8.2f %%" % (name, S.quantile(errs, pct)))
+    print("  %-22s %8.2f %%" % ("max", max(errs)))
+    print("  %-22s %+8.2f %%   (negative: the model under-predicts)" % ("mean signed", _mean([j.signed_pct for j in rows])))
+    print("\n  largest errors:")
+    for j in sorted(rows, key=lambda j: j.abs_pct, reverse=True)[:8]:
+        r = j.record
+        print("    %5sx%-5sx%-5s %3sx%-3sx%-2s w%sx%s s%s   measured %8.1f  predicted %8.1f  %+7.1f%%" % (
+            r["M"], r["N"], r["K"], r["BM"], r["BN"], r["BK"], r["WM"], r["WN"], r["stages"], j.measured,
+            j.predicted, j.signed_pct))
+    classes = error_by_resident_waves(rows)
+    if classes:
+        # The wavefront analogue of the reference's 4-active-warp error class
+        # (README.md:160).
+        print("\n  by resident wavefronts per SIMD and workgroup kind:")
+        for (w, kind), (n, a, sg) in sorted(classes.items()):
+            print("    %4g waves/SIMD  %-20s %4d rows  MAPE %5.1f%%  signed %+6.1f%%" % (w, kind, n, a, sg))
+    print()
+    if mape > mape_ceiling:
+        failed.append("MAPE %.1f%% is above the %.0f%% ceiling" % (mape, mape_ceiling))
+
+    ranking = rank_shapes(rows)
+    print("ranking, per shape (ranges run over predicted ties)")
+    print("  %-28s %8s %7s %13s %16s" % ("shape", "rho", "tie", "best at", "regret@1 %"))
+    for s in ranking:
+        lo, hi = s.best_rank
+        rw, rb = s.regret1
+        print("  %-28s %8s %7d %13s %16s" % (
+            s.tag[:28], "n/a" if s.rho != s.rho else "%.3f" % s.rho, s.largest_tie,
+            str(lo) if lo == hi else "%d-%d" % (lo, hi),
+            "%.1f" % (rw * 100) if s.top_tie == 1 else "%.1f..%.1f" % (rb * 100, rw * 100)))
+    defined = [s.rho for s in ranking if s.rho == s.rho]
+    mean_rho = _mean(defined)
+    worst = max(s.regret1[0] for s in ranking)
+    print("\n  mean rho %.3f over %d shapes (%d without predicted variance)" % (
+        mean_rho, len(defined), len(ranking) - len(defined)))
+    print("  mean regret@1 %.2f%% (ties broken pessimistically), worst %.2f%%" % (
+        _mean([s.regret1[0] for s in ranking]) * 100, worst * 100))
+    print("  largest group of equal predictions: %d configs\n" % max(s.largest_tie for s in ranking))
+    labels = collections.Counter(j.record["pred_bottleneck"] for j in rows)
+    print("predicted bottleneck labels: %s" % ", ".join("%s %d" % kv for kv in labels.most_common()))
+    print("counter cross-check: python -m ridge_amd.labelcheck\n")
+    print(rule)
+    print("MAPE %.2f%%, mean Spearman %.3f, worst regret@1 %.2f%%" % (mape, mean_rho, worst * 100))
+    return failed
 
 
 def main(argv=None):
@@ -150,124 +195,34 @@ def main(argv=None):
     ap.add_argument("--max-mape", type=float, default=10.0)
     ap.add_argument("--fail-mape", type=float, default=15.0)
     ap.add_argument("--no-table-gate", action="store_true",
-                    help="skip the cross-product gate (e.g. for another GPU's sweep)")
+                    help="skip the registered cross-product gate (e.g. for another GPU's sweep)")
     args = ap.parse_args(argv)
-    for p in (args.measured, args.registered):
-        if not os.path.exists(p):
-            sys.exit("missing %s" % p)
-
-    meta = read_meta(args.measured)
-    print("=" * 74)
-    print("ridge model validation")
-    print("=" * 74)
-    for k in ("gpu", "cus", "sms", "nominal_clock_mhz", "warmup_seconds", "canary_drift_fraction"):
-        if k in meta:
-            print("  %-24s %s" % (k, meta[k]))
-    print("  %-24s %s" % ("hardware model", args.hw))
-    print()
-
-    failures = []
-    with tempfile.TemporaryDirectory() as td:
-        pred_path = os.path.join(td, "pred.csv")
-        sys.stderr.write(RM.predict_batch(args.measured, pred_path, hw=args.hw))
-        rows = list(csv.DictReader(r for r in open(pred_path) if not r.startswith("#")))
-    if not rows:
-        sys.exit("no rows after prediction")
-
-    if not args.no_table_gate:
-        registered = load_registered(args.registered)
-        variants = load_variant_table()
-        missing, extra = cross_product_gate(rows, registered, variants)
-        print("registered cross product: %d shapes x %d variants = %d" % (
-            len(registered), len(variants), len(registered) * len(variants)))
-        print("measured rows:            %d" % len(rows))
-        if missing or extra:
-            print("  MISSING from measured: %d, EXTRA in measured: %d" % (len(missing), len(extra)))
-            for m in sorted(missing)[:5]:
-                print("    %s" % (m,))
-            failures.append("measured set does not match the registered sweep")
-        else:
-            print("  matches the registered sweep exactly")
-        print()
-
-    errs, signed = [], []
-    for r in rows:
-        m, p = float(r["tflops"]), float(r["pred_tflops"])
-        r["_abs"] = abs(p - m) / m * 100.0
-        r["_signed"] = (p - m) / m * 100.0
-        errs.append(r["_abs"])
-        signed.append(r["_signed"])
-    mape = sum(errs) / len(errs)
-    print("absolute accuracy")
-    print("  %-22s %8.2f %%   (gate: <= %.0f%%)" % ("MAPE", mape, args.max_mape))
-    print("  %-22s %8.2f %%" % ("median abs error", percentile(errs, 50)))
-    print("  %-22s %8.2f %%" % ("p90 abs error", percentile(errs, 90)))
-    print("  %-22s %8.2f %%" % ("max abs error", max(errs)))
-    print("  %-22s %+8.2f %%   (negative = model under-predicts)" % ("mean signed error", sum(signed) / len(signed)))
-    print()
-    print("  worst 8 configs by absolute error:")
-    print("    %-22s %-22s %9s %9s %8s" % ("shape", "tile/wave tile/stages", "measured", "predicted", "err%"))
-    for r in sorted(rows, key=lambda r: -r["_abs"])[:8]:
-        cfg = "%sx%sx%s w%sx%s s%s" % (r["BM"], r["BN"], r["BK"], r["WM"], r["WN"], r["stages"])
-        print("    %-22s %-22s %9.1f %9.1f %+8.1f" % ("%sx%sx%s" % (r["M"], r["N"], r["K"]), cfg,
-                                                    float(r["tflops"]), float(r["pred_tflops"]), r["_signed"]))
-    print()
-    classes = error_by_resident_waves(rows)
-    if classes:
-        # The wavefront analogue of the reference's 4-active-warp error class
-        # (42 of its 336 A100 rows over-predicted by 39%, README.md:160).
-        print("  by resident wavefronts per SIMD and schedule:")
-        print("    %-11s %-20s %5s %8s %9s" % ("waves/SIMD", "workgroup", "rows", "MAPE %", "signed %"))
-        for (w, sched), (n, a, sg) in sorted(classes.items()):
-            print("    %-11s %-20s %5d %8.1f %+9.1f" % ("%g" % w, sched, n, a, sg))
-        print()
-    if mape > args.fail_mape:
-        failures.append("MAPE %.1f%% is above the %.0f%% ceiling" % (mape, args.fail_mape))
-    elif mape > args.max_mape:
-        print("  note: MAPE %.1f%% exceeds the %.0f%% target (ranking quality is what the pruner uses)\n"
-              % (mape, args.max_mape))
-
-    by_shape = collections.OrderedDict()
-    for r in rows:
-        by_shape.setdefault((r["M"], r["N"], r["K"], r.get("tag", "")), []).append(r)
-    print("ranking quality, per problem shape")
-    print("  %-26s %8s %5s %13s %9s %14s" % ("shape", "spearman", "ties", "rank of best", "recall@3",
-                                             "regret@1 %"))
-    rhos, worst_regrets, ties = [], [], []
-    for (M, N, K, tag), rs in by_shape.items():
-        meas = [float(r["tflops"]) for r in rs]
-        pred = [float(r["pred_tflops"]) for r in rs]
-        rho = spearman(meas, pred)
-        b, w = rank_bounds(rs)
-        wr, br, nt = regret_bounds(rs)
-        largest = max(collections.Counter(round(p, 6) for p in pred).values())
-        rhos.append(rho)
-        worst_regrets.append(wr)
-        ties.append(largest)
-        print("  %-26s %8s %5d %13s %9s %14s" % (
-            (tag or "%sx%sx%s" % (M, N, K))[:26], "  n/a" if rho != rho else "%.3f" % rho, largest,
-            "%d" % b if b == w else "%d-%d" % (b, w), "yes" if w <= 3 else ("maybe" if b <= 3 else "no"),
-            "%.1f-%.1f" % (wr * 100, br * 100) if nt > 1 else "%.1f" % (wr * 100)))
-    valid = [r for r in rhos if r == r]
-    print()
-    print("  %-26s %7.3f   (%d shapes without prediction variance)" % (
-        "mean Spearman", sum(valid) / len(valid) if valid else float("nan"), len(rhos) - len(valid)))
-    print("  %-26s %7.2f %%" % ("worst-case regret@1", max(worst_regrets) * 100))
-    print("  %-26s %7d configs" % ("largest tie group", max(ties)))
-    print()
-    labels = collections.Counter(r["pred_bottleneck"] for r in rows)
-    print("bottleneck attribution")
-    print("  predicted label distribution: %s" % dict(labels))
-    print("  counter cross-check: python -m ridge_amd.labelcheck (registered in data/sweep/rocprof-label-mapping.md)")
-    print()
-    print("=" * 74)
-    print("MAPE %.2f%%, mean Spearman %.3f, worst regret@1 %.2f%%" % (
-        mape, sum(valid) / len(valid) if valid else float("nan"), max(worst_regrets) * 100))
-    if failures:
-        for f in failures:
-            print("  %s" % f)
-        return 1
-    return 0
+    try:
+        meta = T.read(args.measured).meta
+        rows = join(args.measured, args.hw)
+        if not rows:
+            raise T.TableError(args.measured, 0, "no measured rows")
+        gate_lines, failed = [], []
+        if not args.no_table_gate:
+            shapes = T.read_shapes(args.registered)
+            keys = kernel_table_keys()
+            absent, unexpected = registered_gate([j.record for j in rows], shapes, keys)
+            gate_lines.append("registered: %d shapes x %d kernels = %d rows; measured %d rows" % (
+                len(shapes), len(keys), len(shapes) * len(keys), len(rows)))
+            if absent or unexpected:
+                gate_lines.append("  %d registered rows were not measured, %d measured rows were not registered"
+                                  % (len(absent), len(unexpected)))
+                gate_lines += ["    absent: %s" % (a,) for a in sorted(absent)[:5]]
+                failed.append("the measured rows are not the registered cross product")
+            else:
+                gate_lines.append("  the measured rows are exactly the registered cross product")
+            gate_lines.append("")
+    except T.TableError as e:
+        sys.exit(str(e))
+    failed += report(rows, meta, args.hw, gate_lines, args.max_mape, args.fail_mape)
+    for f in failed:
+        print("  FAILED: %s" % f)
+    return 1 if failed else 0
 
 
 if __name__ == "__main__":

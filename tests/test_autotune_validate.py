@@ -1,12 +1,16 @@
-"""Regret and ranking statistics (no GPU): closed forms and hand-made cases,
-including the stable tie order the pruner depends on
-(tools/ridge-autotune.py:93-104, bench/validate.py:36-184)."""
-import csv
+"""Regret and ranking statistics (no GPU): closed forms, hand-made cases,
+independent library implementations and brute force, including the stable tie
+order the pruner depends on (tools/ridge-autotune.py:93-104,
+bench/validate.py:36-184)."""
+import itertools
 import os
+import random
 
 import pytest
 
 from ridge_amd import autotune as AT
+from ridge_amd import stats as S
+from ridge_amd import tables as T
 from ridge_amd import validate as V
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -40,34 +44,107 @@ def test_ties_break_by_table_order():
     assert per == [0.0]
 
 
-def test_average_ranks_and_spearman_textbook():
-    assert V.average_ranks([10, 20, 20, 30]) == [1.0, 2.5, 2.5, 4.0]
-    assert V.spearman([1, 2, 3, 4], [10, 20, 30, 40]) == pytest.approx(1.0)
-    assert V.spearman([1, 2, 3, 4], [4, 3, 2, 1]) == pytest.approx(-1.0)
+def test_midranks_and_spearman_textbook():
+    assert S.midranks([10, 20, 20, 30]) == [1.0, 2.5, 2.5, 4.0]
+    assert S.midranks([3, 3, 3]) == [2.0, 2.0, 2.0]
+    assert S.spearman([1, 2, 3, 4], [10, 20, 30, 40]) == pytest.approx(1.0)
+    assert S.spearman([1, 2, 3, 4], [4, 3, 2, 1]) == pytest.approx(-1.0)
     # Constant prediction has no variance: reported as nan, not 0.
-    r = V.spearman([1, 2, 3], [5, 5, 5])
+    r = S.spearman([1, 2, 3], [5, 5, 5])
     assert r != r
-    # Classic example with ties: x=[1,2,3,4,5], y=[2,1,4,3,5]: d^2 sum = 4 -> 1 - 6*4/(5*24) = 0.8
-    assert V.spearman([1, 2, 3, 4, 5], [2, 1, 4, 3, 5]) == pytest.approx(0.8)
+    # Without ties rho = 1 - 6 sum d^2 / (n (n^2 - 1)): x=[1..5], y=[2,1,4,3,5],
+    # sum d^2 = 4 -> 0.8.
+    assert S.spearman([1, 2, 3, 4, 5], [2, 1, 4, 3, 5]) == pytest.approx(0.8)
 
 
-def test_rank_and_regret_bounds_over_ties():
-    rows = [{"pred_tflops": p, "tflops": m} for p, m in [(9, 50), (9, 100), (8, 70), (7, 60)]]
-    assert V.rank_bounds(rows) == (1, 2)            # best (100) sits in a 2-way top tie
-    worst, best, n = V.regret_bounds(rows)
-    assert n == 2 and worst == pytest.approx(0.5) and best == 0.0
+def test_midranks_and_spearman_match_scipy_on_tied_samples():
+    """scipy's rankdata(method='average') and spearmanr are independent
+    implementations of the same definitions; samples are drawn with heavy ties,
+    as 6-significant-digit predictions produce."""
+    scipy_stats = pytest.importorskip("scipy.stats")
+    rng = random.Random(7)
+    for n in (2, 3, 5, 24, 100):
+        for _ in range(20):
+            a = [rng.choice([1.0, 2.5, 2.5, 3.0, 7.0, 7.0, 9.0]) for _ in range(n)]
+            b = [rng.randint(0, 4) * 1.5 for _ in range(n)]
+            assert S.midranks(a) == pytest.approx(list(scipy_stats.rankdata(a, method="average")))
+            ours = S.spearman(a, b)
+            if len(set(a)) > 1 and len(set(b)) > 1:
+                assert ours == pytest.approx(scipy_stats.spearmanr(a, b)[0], abs=1e-12)
+            else:
+                assert ours != ours
 
 
-def test_cross_product_gate_detects_missing_and_extra():
-    reg = [(256, 256, 64)]
+def test_quantile_against_order_statistics():
+    xs = [5.0, 1.0, 3.0, 2.0, 4.0]
+    assert S.quantile(xs, 50) == 3.0 and S.quantile(xs, 0) == 1.0 and S.quantile(xs, 100) == 5.0
+    assert S.quantile(xs, 90) == pytest.approx(4.6)  # 4 + 0.6 (5 - 4)
+    assert S.quantile([2.0], 90) == 2.0
+    v = S.quantile([], 50)
+    assert v != v
+
+
+def test_expected_random_regret_equals_brute_force():
+    """The closed form against the mean over every k-subset."""
+    rng = random.Random(3)
+    for n in (1, 2, 5, 8):
+        meas = [round(rng.uniform(10, 100), 1) for _ in range(n)]
+        meas[rng.randrange(n)] = meas[0]  # a tie in the measurements
+        best = max(meas)
+        for k in range(1, n + 1):
+            subsets = list(itertools.combinations(meas, k))
+            brute = sum((best - max(c)) / best for c in subsets) / len(subsets)
+            assert S.expected_random_regret(meas, k) == pytest.approx(brute, abs=1e-15)
+    with pytest.raises(ValueError):
+        S.expected_random_regret([1.0, 2.0], 3)
+
+
+def test_rank_and_regret_ranges_over_ties():
+    pred = [9, 9, 8, 7]
+    meas = [50, 100, 70, 60]
+    assert S.best_rank_range(pred, meas) == (1, 2)      # best (100) sits in a 2-way top tie
+    tie = S.top_tie(pred, meas)
+    assert sorted(tie) == [50, 100]
+    assert S.regret(max(meas), min(tie)) == pytest.approx(0.5) and S.regret(max(meas), max(tie)) == 0.0
+    rows = [V.Joined({"tag": "s", "M": "1", "N": "1", "K": "1"}, m, p) for p, m in zip(pred, meas)]
+    (shape,) = V.rank_shapes(rows)
+    assert shape.best_rank == (1, 2) and shape.top_tie == 2 and shape.largest_tie == 2
+    assert shape.regret1 == (pytest.approx(0.5), 0.0)
+
+
+def test_registered_gate_detects_absent_and_unexpected_rows():
+    reg = [(256, 256, 64, "s")]
     variants = [(128, 128, 32, 64, 64, 2, 8), (64, 64, 32, 32, 32, 4, 8)]
     def row(v):
         return dict(zip(("M", "N", "K", "BM", "BN", "BK", "WM", "WN", "stages", "groupM"), map(str, (256, 256, 64) + v)))
-    missing, extra = V.cross_product_gate([row(variants[0])], reg, variants)
-    assert missing == {(256, 256, 64) + variants[1]} and not extra
-    missing, extra = V.cross_product_gate([row(variants[0]), row(variants[1]), row((256, 256, 64, 128, 128, 2, 8))],
-                                          reg, variants)
-    assert not missing and extra == {(256, 256, 64, 256, 256, 64, 128, 128, 2, 8)}
+    absent, unexpected = V.registered_gate([row(variants[0])], reg, variants)
+    assert absent == {(256, 256, 64) + variants[1]} and not unexpected
+    absent, unexpected = V.registered_gate([row(variants[0]), row(variants[1]), row((256, 256, 64, 128, 128, 2, 8))],
+                                           reg, variants)
+    assert not absent and unexpected == {(256, 256, 64, 256, 256, 64, 128, 128, 2, 8)}
+
+
+def test_table_reader_reports_the_line_of_a_ragged_record(tmp_path):
+    p = tmp_path / "t.csv"
+    p.write_text("# gpu,gfx950\n# a comment without a value\nM,N,tflops\n1,2,3.5\n4,5\n")
+    with pytest.raises(T.TableError) as e:
+        T.read(str(p))
+    assert e.value.line == 5 and "2 fields" in str(e.value)
+    p.write_text("# gpu,gfx950\nM,N,tflops\n1,2,x\n")
+    t = T.read(str(p), require=("M", "tflops"))
+    assert t.meta == {"gpu": "gfx950"} and t.number(0, "M", int) == 1
+    with pytest.raises(T.TableError) as e:
+        t.number(0, "tflops")
+    assert e.value.line == 3
+    with pytest.raises(T.TableError):
+        T.read(str(p), require=("K",))
+    p.write_text("# M,N,K,tag,rationale\n64,64,0,bad,zero K\n")
+    with pytest.raises(T.TableError) as e:
+        T.read_shapes(str(p))
+    assert e.value.line == 2
+    p.write_text("# nothing registered\n")
+    with pytest.raises(T.TableError):
+        T.read_shapes(str(p))
 
 
 def test_autotune_end_to_end_on_reference_a100_sweep():
@@ -86,11 +163,10 @@ def test_measured_mi355x_sweep_is_the_registered_cross_product():
     """The committed MI355X sweep covers exactly shapes x table (the measurement
     integrity gate of bench/validate.py:136-156)."""
     path = os.path.join(ROOT, "data", "measured", "mi355x.csv")
-    rows = list(csv.DictReader(l for l in open(path) if not l.startswith("#")))
-    missing, extra = V.cross_product_gate(rows, V.load_registered(os.path.join(ROOT, "data", "sweep",
-                                                                              "mi355x-registered.csv")),
-                                          V.load_variant_table())
-    assert not missing and not extra
+    absent, unexpected = V.registered_gate(T.read(path).records,
+                                           T.read_shapes(os.path.join(ROOT, "data", "sweep", "mi355x-registered.csv")),
+                                           V.kernel_table_keys())
+    assert not absent and not unexpected
 
 
 @pytest.mark.parametrize("name", ["mi355x.csv", "mi355x-replicate.csv"])
@@ -100,11 +176,10 @@ def test_mi355x_pruner_meets_the_target_on_each_measurement(name):
     independent re-measurement taken on another box; both cover the registered
     cross product."""
     path = os.path.join(ROOT, "data", "measured", name)
-    rows = list(csv.DictReader(l for l in open(path) if not l.startswith("#")))
-    missing, extra = V.cross_product_gate(rows, V.load_registered(os.path.join(ROOT, "data", "sweep",
-                                                                              "mi355x-registered.csv")),
-                                          V.load_variant_table())
-    assert not missing and not extra
+    absent, unexpected = V.registered_gate(T.read(path).records,
+                                           T.read_shapes(os.path.join(ROOT, "data", "sweep", "mi355x-registered.csv")),
+                                           V.kernel_table_keys())
+    assert not absent and not unexpected
     table, total, nshapes, per_shape = AT.evaluate(path, os.path.join(ROOT, "data", "hardware", "mi355x.json"))
     assert (total, nshapes) == (336, 14)
     k10 = [r for r in table if r["k"] == 10][0]
@@ -115,11 +190,32 @@ def test_error_classes_by_resident_waves_hand_case():
     """Two 4-wave rows with two resident workgroups (2 waves per SIMD) and one
     8-wave ping-pong row with one (2 per SIMD, its own class): per-class mean of
     |err| and of signed err."""
+    def joined(BM, BN, WM, WN, ctas, sched, measured, predicted):
+        return V.Joined(dict(BM=BM, BN=BN, WM=WM, WN=WN, pred_ctas_per_sm=ctas, schedule=sched), measured, predicted)
     rows = [
-        dict(BM="128", BN="128", WM="64", WN="64", pred_ctas_per_sm="2", schedule="0", _abs=10.0, _signed=10.0),
-        dict(BM="128", BN="128", WM="64", WN="64", pred_ctas_per_sm="2", schedule="0", _abs=20.0, _signed=-20.0),
-        dict(BM="256", BN="256", WM="128", WN="64", pred_ctas_per_sm="1", schedule="1", _abs=5.0, _signed=5.0),
+        joined("128", "128", "64", "64", "2", "0", 100.0, 110.0),
+        joined("128", "128", "64", "64", "2", "0", 100.0, 80.0),
+        joined("256", "256", "128", "64", "1", "1", 100.0, 105.0),
     ]
     got = V.error_by_resident_waves(rows)
-    assert got == {(2.0, "4-wave uniform"): (2, 15.0, -5.0), (2.0, "8-wave ping-pong"): (1, 5.0, 5.0)}
-    assert V.error_by_resident_waves([dict(BM="1")]) == {}
+    assert set(got) == {(2.0, "4-wave uniform"), (2.0, "8-wave ping-pong")}
+    n, mape, signed = got[(2.0, "4-wave uniform")]
+    assert n == 2 and mape == pytest.approx(15.0) and signed == pytest.approx(-5.0)
+    n, mape, signed = got[(2.0, "8-wave ping-pong")]
+    assert n == 1 and mape == pytest.approx(5.0) and signed == pytest.approx(5.0)
+    assert V.error_by_resident_waves([V.Joined(dict(BM="1"), 1.0, 1.0)]) == {}
+
+
+def test_pruner_baselines_on_the_committed_sweep():
+    """The model-free rankings on the committed MI355X sweep: the random
+    shortlist's expected regret is the closed form (2.85% at k = 10, which a
+    sampled estimate of 2,000 draws put at 2.86%), and the model beats every
+    baseline at k = 1."""
+    path = os.path.join(ROOT, "data", "measured", "mi355x.csv")
+    hw = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+    base = AT.baselines(path, hw, ks=(1, 10))
+    assert base[10]["random"][0] == pytest.approx(2.85, abs=0.01)
+    assert base[1]["random"][0] == pytest.approx(22.40, abs=0.01)
+    table, _, _, _ = AT.evaluate(path, hw, ks=(1,))
+    model_k1 = table[0]["mean_regret"]
+    assert all(model_k1 < v[0] for v in base[1].values())

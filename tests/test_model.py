@@ -308,10 +308,25 @@ def test_hardware_json_loader_is_all_or_nothing(tmp_path):
         RM.Hardware(str(bad))
     zero = tmp_path / "z.json"
     zero.write_text(good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 0'))
-    with pytest.raises(ValueError, match="zero or negative"):
+    with pytest.raises(ValueError, match='"clockHz" must be positive'):
         RM.Hardware(str(zero))
-    with pytest.raises(ValueError, match="cannot open"):
+    with pytest.raises(ValueError, match="cannot read"):
         RM.Hardware(str(tmp_path / "missing.json"))
+    # The reader's own error model: every failure names the file and what is wrong.
+    for text, why in [
+        (good.read_text().replace('"numSMs": 256', '"numSMs": 256.5'), '"numSMs" must be an integer'),
+        (good.read_text().replace('"numSMs": 256', '"numSMs": "many"'), '"numSMs" must be an integer'),
+        (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 2.1e9, "clockHz": 1e9'), "appears twice"),
+        (good.read_text().replace('"name": "x"', '"name": {"a": 1}'), "nested objects"),
+        (good.read_text().replace('"name": "x"', '"name": [1]'), "arrays"),
+        (good.read_text() + " {}", "after the end"),
+        (good.read_text().rstrip().rstrip("}"), "not closed"),
+        (good.read_text().replace('"clockHz": 2.1e9', '"clockHz" 2.1e9'), "':' belongs after"),
+    ]:
+        broken = tmp_path / "broken.json"
+        broken.write_text(text)
+        with pytest.raises(ValueError, match=why):
+            RM.Hardware(str(broken))
 
 
 def test_mi355x_persistent_rows_walk_tiles_and_pay_one_fill_and_drain(mi355x):
