@@ -101,6 +101,9 @@ def band_check(res, spec):
                 1.05 * res["ldsControlBytesPerCycle"], "B/cycle/CU", "bounded by the conflict-free control")
     ok &= check("hbmBytesPerSec", res["hbmBytesPerSec"] / 1e12, spec["hbm_bytes_per_sec"] * 0.60 / 1e12,
                 spec["hbm_bytes_per_sec"] * 1.02 / 1e12, "TB/s", "above spec would mean the MALL, not HBM")
+    if "hbmWriteBytesPerSec" in res:
+        ok &= check("hbmWriteBytesPerSec", res["hbmWriteBytesPerSec"] / 1e12, spec["hbm_bytes_per_sec"] * 0.40 / 1e12,
+                    spec["hbm_bytes_per_sec"] * 1.02 / 1e12, "TB/s", "streaming stores over 4 GiB")
     ok &= check("warpsNeededToHide", res["warpsNeededToHide"], 1, 32, "waves/CU")
     # The L2s serve faster than HBM (at the loaded clock); 8 XCDs x 16 channels x
     # 128 B per cycle is the ceiling.
@@ -192,6 +195,8 @@ def hardware_json(res, spec, arch):
     }
     for key in CLOCK_RATIO_KEYS:
         out[key] = res[key]
+    if "hbmWriteBytesPerSec" in res:  # measured by cal-hbm-bw's write sweep
+        out["hbmWriteBytesPerSec"] = res["hbmWriteBytesPerSec"]
     for key in SKELETON_KEYS:
         if key in res:
             out[key] = res[key]

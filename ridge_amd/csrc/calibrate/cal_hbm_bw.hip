@@ -3,12 +3,25 @@
 // Counterpart of the reference's bench/calibrate/cal-hbm-bw.cu:22-109: a
 // grid-stride 16-byte streaming read over a 4 GiB buffer, far beyond both the
 // 4 MiB L2 of each XCD and the 256 MiB shared MALL, so the reads come from HBM;
-// 7 timed repeats, median. A 64 MiB buffer (MALL-resident) is also timed and
-// reported as information: that is the level that serves cross-XCD panel
-// re-reads in the GEMM. l2HitBytesPerCycle times the same kind of read (16 GiB of
-// it) with every index wrapped into a 1 MiB buffer, which each XCD's L2 holds, in
-// shader cycles: the rate at which the L2s serve tiles that every workgroup
-// re-reads (the shared operand of a skinny GEMM).
+// 7 timed repeats, middle value.
+//
+// HBM only reaches its rate with enough bytes in flight (Little's law: ~8 TB/s
+// times a loaded latency of a few microseconds is tens of MB across the chip).
+// A loop that issues one 16-byte load per lane and waits for it before the next
+// holds about 32 KiB per CU in flight and measures the loop, not the memory. So
+// the read is swept over the number of independent loads each lane keeps in
+// flight (1..16, separate accumulators, all issued before any is consumed),
+// the workgroups per CU (2, 4, 8 of 256 lanes) and the load's cache policy
+// (default, non-temporal); every point is printed as a CAL_CURVE line and the
+// constant is the largest middle value whose repeats are stable.
+//
+// hbmWriteBytesPerSec is the same sweep for 16-byte streaming stores (a GEMM
+// writes its C this way). A 64 MiB buffer (MALL-resident) is also timed and reported as information:
+// that is the level that serves cross-XCD panel re-reads in the GEMM.
+// l2HitBytesPerCycle times the same kind of read (16 GiB of it) with every index
+// wrapped into a 1 MiB buffer, which each XCD's L2 holds, in shader cycles: the
+// rate at which the L2s serve tiles that every workgroup re-reads (the shared
+// operand of a skinny GEMM).
 #include "cal_common.hpp"
 
 using namespace ridgecal;
@@ -17,12 +30,61 @@ namespace {
 
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-__global__ void streamReadKernel(const float4_t* __restrict__ src, size_t n, float* sink) {
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    const size_t stride = size_t(gridDim.x) * blockDim.x;
-    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) acc += src[i];
-    const float s = acc[0] + acc[1] + acc[2] + acc[3];
-    if (s == 1.2345678e30f) sink[0] = s;
+constexpr int kLanes = 256;
+
+// Flight independent 16-byte loads per lane per pass: lane t of workgroup g reads
+// chunks base + j * stride (j < Flight), stride = all lanes of the grid, then
+// moves on by Flight * stride. `passes` * Flight * stride chunks are read in all;
+// the host sizes `passes` so that this stays inside the buffer.
+template <int Flight, bool NonTemporal>
+__global__ __launch_bounds__(kLanes) void streamReadKernel(const float4_t* __restrict__ src, size_t passes,
+                                                           float* sink) {
+    const size_t stride = size_t(gridDim.x) * kLanes;
+    const float4_t* p = src + size_t(blockIdx.x) * kLanes + threadIdx.x;
+    float4_t acc[Flight];
+#pragma unroll
+    for (int j = 0; j < Flight; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (size_t pass = 0; pass < passes; ++pass) {
+        float4_t v[Flight];
+#pragma unroll
+        for (int j = 0; j < Flight; ++j) {
+            if constexpr (NonTemporal)
+                v[j] = __builtin_nontemporal_load(p + j * stride);
+            else
+                v[j] = p[j * stride];
+        }
+        // Keeps the scheduler from sinking each add up to its load, which would
+        // put a full wait after every load and leave one in flight.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < Flight; ++j) acc[j] += v[j];
+        p += Flight * stride;
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < Flight; ++j) total += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    if (total == -1.0e38f) sink[0] = total;
+}
+
+// The write counterpart: Flight 16-byte stores per lane per pass, laid out as the
+// reads are. The stored values differ per lane and per pass, so the write path
+// carries toggling data as a GEMM's C does.
+template <int Flight, bool NonTemporal>
+__global__ __launch_bounds__(kLanes) void streamWriteKernel(float4_t* __restrict__ dst, size_t passes) {
+    const size_t stride = size_t(gridDim.x) * kLanes;
+    float4_t* p = dst + size_t(blockIdx.x) * kLanes + threadIdx.x;
+    float4_t v = {float(threadIdx.x), float(blockIdx.x), 0.5f, -0.25f};
+    for (size_t pass = 0; pass < passes; ++pass) {
+#pragma unroll
+        for (int j = 0; j < Flight; ++j) {
+            if constexpr (NonTemporal)
+                __builtin_nontemporal_store(v, p + j * stride);
+            else
+                p[j * stride] = v;
+        }
+        v[2] += 1.0f;
+        p += Flight * stride;
+    }
 }
 
 // The same read over `n` float4 positions, each wrapped into the first `mask + 1`
@@ -40,7 +102,7 @@ __global__ __launch_bounds__(256) void wrappedReadKernel(const float4_t* __restr
     const uint64_t c1 = cycles();
     const uint64_t r1 = realtime();
     const float s = acc[0] + acc[1] + acc[2] + acc[3];
-    if (s == 1.2345678e30f) sink[0] = s;
+    if (s == -1.0e38f) sink[0] = s;
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
 }
 
@@ -63,17 +125,45 @@ double l2BytesPerCycle(const float4_t* src, size_t bytes, size_t wrapBytes, floa
         reps.push_back(double(bytes) / cyc);
         clocks.push_back(hz);
     }
-    clockHz = median(clocks);
-    return median(reps);
+    clockHz = middle(clocks);
+    return middle(reps);
 }
 
-double timeRead(const float4_t* src, size_t bytes, float* sink, int blocks, std::vector<double>& reps) {
+struct ReadPoint {
+    int flight = 0, wgPerCu = 0;
+    bool nonTemporal = false;
+    double bytesPerSec = 0.0;
+    std::vector<double> reps;
+};
+
+// Middle over kRepeats of one streaming configuration (reads, or writes when
+// Write) over the first `bufBytes` of `buf` (whole passes only; the bytes
+// actually moved are counted).
+template <int Flight, bool NonTemporal, bool Write = false>
+ReadPoint timeRead(float4_t* buf, size_t bufBytes, float* sink, int cus, int wgPerCu) {
+    ReadPoint pt;
+    pt.flight = Flight;
+    pt.wgPerCu = wgPerCu;
+    pt.nonTemporal = NonTemporal;
+    const int blocks = cus * wgPerCu;
+    const size_t chunksPerPass = size_t(blocks) * kLanes * Flight;
+    const size_t passes = bufBytes / sizeof(float4_t) / chunksPerPass;
+    if (passes == 0) {
+        std::fprintf(stderr, "buffer of %zu bytes is smaller than one pass of %zu chunks\n", bufBytes, chunksPerPass);
+        std::exit(2);
+    }
+    const double bytes = double(passes * chunksPerPass * sizeof(float4_t));
     hipEvent_t e0, e1;
     CAL_HIP_CHECK(hipEventCreate(&e0));
     CAL_HIP_CHECK(hipEventCreate(&e1));
-    const size_t n = bytes / sizeof(float4_t);
-    reps.clear();
-    auto launch = [&]() { hipLaunchKernelGGL(streamReadKernel, dim3(blocks), dim3(256), 0, nullptr, src, n, sink); };
+    auto launch = [&]() {
+        if constexpr (Write)
+            hipLaunchKernelGGL((streamWriteKernel<Flight, NonTemporal>), dim3(blocks), dim3(kLanes), 0, nullptr, buf,
+                               passes);
+        else
+            hipLaunchKernelGGL((streamReadKernel<Flight, NonTemporal>), dim3(blocks), dim3(kLanes), 0, nullptr, buf,
+                               passes, sink);
+    };
     for (int r = 0; r < kRepeats; ++r) {
         launch();
         CAL_HIP_CHECK(hipDeviceSynchronize());
@@ -84,11 +174,46 @@ double timeRead(const float4_t* src, size_t bytes, float* sink, int blocks, std:
         CAL_HIP_CHECK(hipGetLastError());
         float ms = 0.0f;
         CAL_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
-        reps.push_back(double(bytes) / (double(ms) * 1e-3));
+        pt.reps.push_back(bytes / (double(ms) * 1e-3));
     }
     CAL_HIP_CHECK(hipEventDestroy(e0));
     CAL_HIP_CHECK(hipEventDestroy(e1));
-    return median(reps);
+    pt.bytesPerSec = middle(pt.reps);
+    return pt;
+}
+
+// The largest middle value among points whose repeats are stable, or null.
+const ReadPoint* stableMaximum(const std::vector<ReadPoint>& curve) {
+    const ReadPoint* best = nullptr;
+    for (const ReadPoint& pt : curve)
+        if (dispersion(pt.reps) <= 0.05 && (!best || pt.bytesPerSec > best->bytesPerSec)) best = &pt;
+    return best;
+}
+
+void printCurve(const char* what, const std::vector<ReadPoint>& curve) {
+    for (const ReadPoint& pt : curve) {
+        const double d = dispersion(pt.reps);
+        std::printf("  %8d %10d %6d %12.1f %9.1f%%\n", pt.flight, pt.wgPerCu, int(pt.nonTemporal),
+                    pt.bytesPerSec / 1e9, d * 100.0);
+        std::printf("CAL_CURVE %s flight %d wgPerCu %d nonTemporal %d bytesPerSec %.6e dispersion %.4f\n", what,
+                    pt.flight, pt.wgPerCu, int(pt.nonTemporal), pt.bytesPerSec, d);
+    }
+}
+
+template <bool NonTemporal>
+void sweepFlight(std::vector<ReadPoint>& out, float4_t* src, size_t bytes, float* sink, int cus, int wgPerCu) {
+    out.push_back(timeRead<1, NonTemporal>(src, bytes, sink, cus, wgPerCu));
+    out.push_back(timeRead<2, NonTemporal>(src, bytes, sink, cus, wgPerCu));
+    out.push_back(timeRead<4, NonTemporal>(src, bytes, sink, cus, wgPerCu));
+    out.push_back(timeRead<8, NonTemporal>(src, bytes, sink, cus, wgPerCu));
+    out.push_back(timeRead<16, NonTemporal>(src, bytes, sink, cus, wgPerCu));
+}
+
+template <bool NonTemporal>
+void sweepWrites(std::vector<ReadPoint>& out, float4_t* dst, size_t bytes, int cus, int wgPerCu) {
+    out.push_back(timeRead<1, NonTemporal, true>(dst, bytes, nullptr, cus, wgPerCu));
+    out.push_back(timeRead<2, NonTemporal, true>(dst, bytes, nullptr, cus, wgPerCu));
+    out.push_back(timeRead<4, NonTemporal, true>(dst, bytes, nullptr, cus, wgPerCu));
 }
 
 }  // namespace
@@ -110,17 +235,52 @@ int main() {
     CAL_HIP_CHECK(hipMalloc(&sink, sizeof(float)));
     CAL_HIP_CHECK(hipMemset(src, 1, kBytes));
     warmUp();
-    const int blocks = prop.multiProcessorCount * 32;
-    std::printf("\nHBM streaming read, %.2f GiB buffer, %d blocks x 256 workitems, 16-byte loads\n",
-                kBytes / double(1ull << 30), blocks);
-    std::vector<double> reps;
-    const double hbm = timeRead(src, kBytes, sink, blocks, reps);
-    for (size_t i = 0; i < reps.size(); ++i) std::printf("  repeat %zu %10.1f GB/s\n", i, reps[i] / 1e9);
-    const bool stable = reportConstant("hbmBytesPerSec", hbm / 1e9, "GB/s", reps);
+    const int cus = prop.multiProcessorCount;
+    std::printf("\nHBM streaming read, %.2f GiB buffer, 256-lane workgroups, 16-byte loads\n",
+                kBytes / double(1ull << 30));
+    std::printf("  %8s %10s %6s %12s %10s\n", "in flight", "WG per CU", "nt", "GB/s", "range");
+    std::vector<ReadPoint> curve;
+    for (int wgPerCu : {2, 4, 8}) {
+        sweepFlight<false>(curve, src, kBytes, sink, cus, wgPerCu);
+        sweepFlight<true>(curve, src, kBytes, sink, cus, wgPerCu);
+    }
+    printCurve("hbmRead", curve);
+    const ReadPoint* best = stableMaximum(curve);
+    if (!best) {
+        std::fprintf(stderr, "no configuration of the HBM read had stable repeats\n");
+        return 1;
+    }
+    const double hbm = best->bytesPerSec;
+    std::printf("\nlargest stable point: %d loads in flight per lane, %d workgroups per CU, %s loads\n",
+                best->flight, best->wgPerCu, best->nonTemporal ? "non-temporal" : "default");
+    for (size_t i = 0; i < best->reps.size(); ++i) std::printf("  repeat %zu %10.1f GB/s\n", i, best->reps[i] / 1e9);
+    const bool stable = reportConstant("hbmBytesPerSec", hbm / 1e9, "GB/s", best->reps);
     std::printf("  %-24s %12.1f GB/s (datasheet, cross-check only)\n", "MI355X HBM3E", 8000.0);
     std::printf("  %-24s %12.1f %%\n", "achieved vs datasheet", 100.0 * hbm / 8.0e12);
-    std::vector<double> mallReps;
-    const double mall = timeRead(src, kMallBytes, sink, blocks, mallReps);
+    // Streaming writes over the same 4 GiB, the stream a GEMM's C is: its own
+    // ceiling, since HBM turns the bus around between reads and writes and the
+    // two directions do not reach the same rate.
+    std::printf("\nHBM streaming write, %.2f GiB buffer, 256-lane workgroups, 16-byte stores\n",
+                kBytes / double(1ull << 30));
+    std::printf("  %8s %10s %6s %12s %10s\n", "per pass", "WG per CU", "nt", "GB/s", "range");
+    std::vector<ReadPoint> writes;
+    for (int wgPerCu : {2, 4, 8}) {
+        sweepWrites<false>(writes, src, kBytes, cus, wgPerCu);
+        sweepWrites<true>(writes, src, kBytes, cus, wgPerCu);
+    }
+    printCurve("hbmWrite", writes);
+    const ReadPoint* bestWrite = stableMaximum(writes);
+    if (!bestWrite) {
+        std::fprintf(stderr, "no configuration of the HBM write had stable repeats\n");
+        return 1;
+    }
+    const double hbmWrite = bestWrite->bytesPerSec;
+    std::printf("\nlargest stable point: %d stores per lane per pass, %d workgroups per CU, %s stores\n",
+                bestWrite->flight, bestWrite->wgPerCu, bestWrite->nonTemporal ? "non-temporal" : "default");
+    const bool writeStable = reportConstant("hbmWriteBytesPerSec", hbmWrite / 1e9, "GB/s", bestWrite->reps);
+    CAL_HIP_CHECK(hipMemset(src, 1, kBytes));
+    const ReadPoint mallPt = timeRead<4, false>(src, kMallBytes, sink, cus, 8);
+    const double mall = mallPt.bytesPerSec;
     std::printf("  %-24s %12.1f GB/s (64 MiB, MALL-resident, information only)\n", "mallBytesPerSec", mall / 1e9);
     // 16 GiB of reads wrapped into 1 MiB, which each XCD's 4 MiB L2 holds, on 8
     // workgroups of 256 per CU (all resident). A rate in bytes per second follows
@@ -140,9 +300,10 @@ int main() {
                 l2 * l2Clock / 1e12, l2Clock / 1e6);
     CAL_HIP_CHECK(hipFree(dStamps));
     std::printf("\nCAL_RESULT hbmBytesPerSec %.6e\n", hbm);
+    std::printf("CAL_RESULT hbmWriteBytesPerSec %.6e\n", hbmWrite);
     std::printf("CAL_RESULT mallBytesPerSec %.6e\n", mall);
     std::printf("CAL_RESULT l2HitBytesPerCycle %.6f\n", l2);
     CAL_HIP_CHECK(hipFree(src));
     CAL_HIP_CHECK(hipFree(sink));
-    return stable && l2Stable ? 0 : 1;
+    return stable && writeStable && l2Stable ? 0 : 1;
 }
