@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Headline benchmark: FP16 GEMM TFLOP/s at 4096^3 on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant BM,BN,BK,WM,WN,S,G]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--repeats R] [--variant BM,BN,BK,WM,WN,S,G]
                     [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt] [--no-cold]
                     [--operands uniform|zeros|ones]
                     [--allow-partitioned]
@@ -10,12 +10,15 @@
 
 A step is one C = A * B launch (FP16 A, B row-major from a seeded U[-1,1) device
 fill, FP32 accumulate, FP16 C) through the C ABI, with inputs resident in HBM
-before the timed region. W untimed steps, then exactly K timed steps bracketed by
-torch.cuda.synchronize(); value = 2 M N K K / elapsed. The same launches are also
-bracketed by HIP events on the launch stream for the roofline figure, and the
-hipBLASLt comparator (best of its heuristic candidates, best of a before and an
-after reading, as the reference does in bench/check-gemm.cu:357-391) is timed the
-same way. Prints ONE JSON line.
+before the timed region. 5 s of the same launches to bring the clock to its
+loaded state, W untimed steps, then --repeats (default 5) windows of exactly K
+steps, each bracketed by torch.cuda.synchronize(); value = 2 M N K K / elapsed of
+the middle window, with the fastest and slowest windows in `spread`. The same
+launches are also bracketed by HIP events on the launch stream for the roofline
+figure. The hipBLASLt comparator (best of its heuristic candidates, best of a
+before and an after reading, as the reference does in
+bench/check-gemm.cu:357-391) is timed the same way and compared on the same basis
+(wall clock warm, HIP events cold). Prints ONE JSON line.
 
 cold: the same launches (ours and hipBLASLt's) rotated over enough operand sets
 that twice the 256 MB MALL is touched between two uses of one set, so every
@@ -86,6 +89,32 @@ def time_launches(fn, steps, stream):
     return wall, e0.elapsed_time(e1)
 
 
+def middle(xs):
+    """Middle order statistic (mean of the two central values for an even count)."""
+    ys = sorted(xs)
+    h = len(ys) // 2
+    return ys[h] if len(ys) % 2 else 0.5 * (ys[h - 1] + ys[h])
+
+
+def time_windows(fn, steps, stream, repeats):
+    """`repeats` windows of exactly `steps` launches each. Returns per-launch wall
+    and HIP-event milliseconds, one entry per window, in the order timed."""
+    wall_ms, event_ms = [], []
+    for _ in range(repeats):
+        wall, ev = time_launches(fn, steps, stream)
+        wall_ms.append(wall * 1e3 / steps)
+        event_ms.append(ev / steps)
+    return wall_ms, event_ms
+
+
+def window_summary(flops, per_launch_ms):
+    """TFLOP/s of the middle window, with the fastest and slowest windows."""
+    rates = [flops / (ms * 1e-3) / 1e12 for ms in per_launch_ms]
+    mid = middle(rates)
+    return {"tflops": round(mid, 3), "min": round(min(rates), 3), "max": round(max(rates), 3),
+            "range_pct": round((max(rates) - min(rates)) / mid * 100, 2), "windows": len(rates)}
+
+
 def calibrated_peaks():
     """The calibrated chip's own ceilings (data/hardware/mi355x.json): the MFMA
     rate a pure matrix load sustains at its loaded clock, and the HBM copy rate."""
@@ -152,23 +181,36 @@ def cold_sets(set_bytes):
     return max(3, 1 + -(-2 * MALL_BYTES // set_bytes))
 
 
-def time_cold(make_step, sets, steps, stream):
+def time_cold(make_step, sets, steps, stream, repeats, warm_seconds):
     """HIP-event milliseconds per launch with launch i on operand set i % len(sets),
-    so no launch finds its A, B or C in the MALL or the L2s."""
+    so no launch finds its A, B or C in the MALL or the L2s; one entry per window
+    of `steps` launches (the rotation continues across windows). The rotation
+    first runs for `warm_seconds`: allocating and filling the extra sets leaves
+    the GPU idle long enough for its clock to drop, and without this the first
+    windows time the clock's ramp rather than the cold caches."""
     import torch
     n = len(sets)
     fns = [make_step(*s) for s in sets]
-    for i in range(2 * n):
-        fns[i % n]()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(steps):
-        fns[i % n]()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    t0 = time.perf_counter()
+    while True:
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_seconds:
+            break
+    out = []
+    j = 0
+    for _ in range(repeats):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fns[j % n]()
+            j += 1
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) / steps)
+    return out
 
 
 def cpu_threads():
@@ -290,7 +332,11 @@ def main():
     ap.add_argument("--shape", default=",".join(str(x) for x in DEFAULT_SHAPE))
     ap.add_argument("--operands", default="uniform", choices=["uniform", "zeros", "ones"],
                     help="operand data; anything but the default is a power-limit probe, not the metric")
-    ap.add_argument("--warm-seconds", type=float, default=3.0)
+    ap.add_argument("--warm-seconds", type=float, default=5.0)
+    ap.add_argument("--cold-warm-seconds", type=float, default=2.0,
+                    help="seconds the cold rotation runs before its windows are timed (capped by --warm-seconds)")
+    ap.add_argument("--repeats", type=int, default=5,
+                    help="timed windows of --steps launches each; figures are the middle window")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-blaslt", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
@@ -346,13 +392,14 @@ def main():
         if rc != 0:
             raise SystemExit("ridge_gemm_launch returned %d" % rc)
 
-    # Clock ramp: a few seconds of the same work before anything is timed
-    # (the reference warms 5 s, check-gemm.cu:41-45).
+    # Clock ramp: seconds of the same work before anything is timed (the
+    # reference warms 5 s, check-gemm.cu:41-45).
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < args.warm_seconds:
         for _ in range(50):
             step()
         torch.cuda.synchronize()
+    repeats = max(1, args.repeats)
 
     blas = None
     blas_before = blas_after = None
@@ -372,18 +419,20 @@ def main():
 
         for _ in range(args.warmup):
             blas_step()
-        _, ms = time_launches(blas_step, args.steps, stream)
-        blas_before = flops * args.steps / (ms * 1e-3) / 1e12
+        blas_before, _ = time_windows(blas_step, args.steps, stream, repeats)
 
+    # The timed region proper: W untimed steps, then `repeats` windows of exactly
+    # K steps, each bracketed by torch.cuda.synchronize(); `value` is the middle
+    # window's wall-clock rate.
     for _ in range(args.warmup):
         step()
-    wall, ev_ms = time_launches(step, args.steps, stream)
-    value = flops * args.steps / wall / 1e12
-    per_launch_ms = ev_ms / args.steps
+    wall_ms, event_ms = time_windows(step, args.steps, stream, repeats)
+    mid_wall_ms = middle(wall_ms)
+    value = flops / (mid_wall_ms * 1e-3) / 1e12
+    per_launch_ms = middle(event_ms)
 
     if blas is not None:
-        _, ms = time_launches(blas_step, args.steps, stream)
-        blas_after = flops * args.steps / (ms * 1e-3) / 1e12
+        blas_after, _ = time_windows(blas_step, args.steps, stream, repeats)
         blas.close()
 
     # Cold: the same launches rotated over operand sets that together exceed
@@ -410,9 +459,13 @@ def main():
             return f
 
         cold_steps = max(args.steps // 4, 4 * n_sets)
-        cold_ms = time_cold(make_step, sets, cold_steps, stream)
+        cold_warm_s = max(0.0, min(args.cold_warm_seconds, args.warm_seconds))
+        cold_windows = time_cold(make_step, sets, cold_steps, stream, repeats, cold_warm_s)
+        cold_ms = middle(cold_windows)
         cold = {"tflops": round(flops / (cold_ms * 1e-3) / 1e12, 3), "ms_per_launch": round(cold_ms, 6),
-                "sets": n_sets, "set_bytes": set_bytes, "launches": cold_steps,
+                "spread": window_summary(flops, cold_windows),
+                "sets": n_sets, "set_bytes": set_bytes, "launches_per_window": cold_steps,
+                "rotation_warm_seconds": cold_warm_s,
                 "roofline": roofline(M, N, K, cold_ms, None)}
         if blas is not None:
             try:
@@ -426,7 +479,7 @@ def main():
             def make_blas_step(a, b, c):
                 return lambda: blas.gemm(a, b, c, M, N, K, stream=stream)
 
-            blas_cold_ms = time_cold(make_blas_step, sets, cold_steps, stream)
+            blas_cold_ms = middle(time_cold(make_blas_step, sets, cold_steps, stream, repeats, cold_warm_s))
             blas.close()
             cold["hipblaslt_tflops"] = round(flops / (blas_cold_ms * 1e-3) / 1e12, 3)
             cold["frac_of_hipblaslt"] = round(blas_cold_ms / cold_ms, 4)
@@ -442,7 +495,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 6),
+        "ms_per_step": round(mid_wall_ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -453,16 +506,23 @@ def main():
                  % ("0" if args.operands == "zeros" else "1/64")),
         "config": {"workload": "FP16 GEMM M=%d N=%d K=%d, row-major A/B/C, FP32 accumulate, FP16 C" % (M, N, K),
                    "variant": v.label(), "parallelism": "single GPU"},
+        "repeats": repeats,
+        "spread": window_summary(flops, wall_ms),
+        "warm_seconds": args.warm_seconds,
         "frac_of_mfma_peak": round(value / PEAK_FP16_TFLOPS, 4),
         "roofline": roofline(M, N, K, per_launch_ms, traffic),
     }
     if blas_error is not None:
         out["hipblaslt"] = {"error": blas_error}
     if blas_before is not None:
-        best = max(blas_before, blas_after)
-        out["hipblaslt"] = {"tflops": round(best, 3), "before": round(blas_before, 3),
-                            "after": round(blas_after, 3),
-                            "drift": round(abs(blas_after - blas_before) / blas_before, 4),
+        # Same basis as `value`: the middle window's wall-clock rate, best of the
+        # readings before and after ours (bench/check-gemm.cu:357-391).
+        before = flops / (middle(blas_before) * 1e-3) / 1e12
+        after = flops / (middle(blas_after) * 1e-3) / 1e12
+        best = max(before, after)
+        out["hipblaslt"] = {"tflops": round(best, 3), "before": round(before, 3), "after": round(after, 3),
+                            "drift": round(abs(after - before) / before, 4),
+                            "spread": window_summary(flops, blas_before if before >= after else blas_after),
                             "frac_of_hipblaslt": round(value / best, 4)}
     if cold is not None:
         out["cold"] = cold
