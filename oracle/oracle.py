@@ -128,6 +128,43 @@ def passes(got, ref, max_abs_a, max_abs_b, K):
     return ok, frob, mx, ne
 
 
+# FP16-output gate (this build's, tighter than the reference's): FP16 x FP16
+# products are exact in FP32; an FP32 sum of K of them is within
+# K * 2^-24 * sum_k |a_ik| |b_kj| of the exact sum (the a-priori bound
+# gamma_K = K u / (1 - K u), u = 2^-24, whose denominator is below 1.001 for
+# K <= 2^14); rounding that sum to FP16 adds at most 2^-11 of its magnitude, or
+# 2^-25 absolute below the normal range. Any kernel that accumulates in FP32
+# and rounds once meets the bound element by element; its relative Frobenius
+# error is then of order 2^-11 / sqrt(3), about 3e-4, hence the 1e-3 gate.
+FP16_FROB_TOL = 1e-3
+_U32 = 2.0 ** -24
+_U16 = 2.0 ** -11
+
+
+def abs_bits(bits):
+    """FP16 bit patterns with the sign bit cleared (|x| for every half)."""
+    return np.ascontiguousarray(bits, dtype=np.uint16) & np.uint16(0x7FFF)
+
+
+def fp16_output_bound(ref, absprod, K):
+    """Per-element bound |got - ref| for an FP32-accumulated, once-rounded FP16
+    result: ref = A B and absprod = |A| |B| (both f64, from gemm_f64)."""
+    accum = 1.001 * K * _U32 * np.asarray(absprod, dtype=np.float64)
+    return _U16 * (np.abs(ref) + accum) + accum + 2.0 ** -25
+
+
+def passes_fp16(got, ref, absprod, K):
+    """The FP16-output gate: relative Frobenius <= 1e-3 and every element within
+    fp16_output_bound. Returns (ok, frob, worst), worst = max |err| / bound."""
+    got = np.asarray(got, dtype=np.float64).reshape(np.shape(ref))
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(got - ref)
+    den = np.sqrt(np.sum(ref * ref))
+    frob = float(np.sqrt(np.sum(err * err)) / den) if den > 0 else float(np.any(err > 0))
+    worst = float(np.max(err / fp16_output_bound(ref, absprod, K))) if err.size else 0.0
+    return frob <= FP16_FROB_TOL and worst <= 1.0, frob, worst
+
+
 def selftest_ref(n=4096):
     out = np.empty(n, dtype=np.float64)
     lib().oracle_selftest_ref(out, n)

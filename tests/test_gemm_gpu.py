@@ -185,14 +185,50 @@ def test_baseline_configs_uniform_inputs(M, N, K):
     G.fill_uniform(B, 2)
     Ab, Bb = _bits(A), _bits(B)
     rows = np.arange(M) if M <= 1024 else np.linspace(0, M - 1, 64).astype(int)
-    ref = O.gemm_f64(Ab.reshape(M, K)[rows].ravel(), Bb, len(rows), N, K)
+    Arows = Ab.reshape(M, K)[rows].ravel()
+    ref = O.gemm_f64(Arows, Bb, len(rows), N, K)
+    absprod = O.gemm_f64(O.abs_bits(Arows), O.abs_bits(Bb), len(rows), N, K)
+    max_a, max_b = _max_abs(Ab), _max_abs(Bb)
     for v in G.variants():
         if not v.divides(M, N, K):
             continue
         C = _run(v.index, A, B, M, N, K)
         got = O.f16_bits_to_f32(_bits(C)).reshape(M, N)[rows]
-        ok, frob, mx, ne = O.passes(got, ref, 1.0, 1.0, K)
+        ok, frob, mx, ne = O.passes(got, ref, max_a, max_b, K)
         assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
+        ok, frob, worst = O.passes_fp16(got, ref, absprod, K)
+        assert ok, "%s on %dx%dx%d: FP16-output gate frob %.3e, worst element at %.2f of its bound" % (
+            v.label(), M, N, K, frob, worst)
+
+
+def test_headline_variant_every_output_at_4096_cubed():
+    """The bench's variant at 4096^3 on U[-1,1) inputs: all 16.8 M outputs against
+    the f64 oracle under the reference's gates and the FP16-output gate (every
+    element within its FP32-accumulation-plus-one-rounding bound, Frobenius
+    <= 1e-3)."""
+    M = N = K = 4096
+    idx = G.find_variant(256, 256, 32, 128, 64, 3, 4)
+    assert idx >= 0
+    print("headline %s every output" % G.variant(idx).label(), flush=True)
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, 1)
+    G.fill_uniform(B, 2)
+    Ab, Bb = _bits(A), _bits(B)
+    got = O.f16_bits_to_f32(_bits(_run(idx, A, B, M, N, K))).reshape(M, N)
+    ref = O.gemm_f64(Ab, Bb, M, N, K)
+    ok, frob, mx, ne = O.passes(got, ref, _max_abs(Ab), _max_abs(Bb), K)
+    assert ok, "reference gates: frob %.3e maxRel %.3e norm %.3e" % (frob, mx, ne)
+    absprod = O.gemm_f64(O.abs_bits(Ab), O.abs_bits(Bb), M, N, K)
+    ok, frob, worst = O.passes_fp16(got, ref, absprod, K)
+    print("  frob %.3e, worst element at %.3f of its bound" % (frob, worst), flush=True)
+    assert ok, "FP16-output gate: frob %.3e, worst element at %.2f of its bound" % (frob, worst)
+
+
+def _max_abs(bits):
+    """max |x| over FP16 bit patterns (the reference's normalisation,
+    check-gemm.cu:110-135, taken from the operands actually used)."""
+    return float(np.max(np.abs(O.f16_bits_to_f32(bits))))
 
 
 def test_hipblaslt_comparator_agrees_with_oracle():
@@ -238,15 +274,21 @@ def test_registered_sweep_shapes_every_variant(M, N, K):
     G.fill_uniform(B, 12)
     rows = np.linspace(0, M - 1, 16).astype(int)
     Ab = A[torch.from_numpy(rows).to(DEV)].cpu().view(torch.int16).numpy().view(np.uint16).ravel()
-    ref = O.gemm_f64(Ab, _bits(B), len(rows), N, K)
+    Bb = _bits(B)
+    ref = O.gemm_f64(Ab, Bb, len(rows), N, K)
+    absprod = O.gemm_f64(O.abs_bits(Ab), O.abs_bits(Bb), len(rows), N, K)
+    max_a, max_b = _max_abs(_bits(A)), _max_abs(Bb)
     idx = torch.from_numpy(rows).to(DEV)
     for v in G.variants():
         assert v.divides(M, N, K), v.label()
         C = _run(v.index, A, B, M, N, K)
         assert not bool(torch.isnan(C).any()), "%s left outputs unwritten at %dx%dx%d" % (v.label(), M, N, K)
         got = O.f16_bits_to_f32(C[idx].cpu().view(torch.int16).numpy().view(np.uint16)).reshape(len(rows), N)
-        ok, frob, mx, ne = O.passes(got, ref, 1.0, 1.0, K)
+        ok, frob, mx, ne = O.passes(got, ref, max_a, max_b, K)
         assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
+        ok, frob, worst = O.passes_fp16(got, ref, absprod, K)
+        assert ok, "%s on %dx%dx%d: FP16-output gate frob %.3e, worst element at %.2f of its bound" % (
+            v.label(), M, N, K, frob, worst)
         del C
 
 

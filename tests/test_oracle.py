@@ -168,3 +168,49 @@ def test_normalized_max_err():
     ref = np.array([0.0, 1.0, -2.0])
     got = np.array([0.0, 1.5, -2.0], np.float32)
     assert O.normalized_max_err(got, ref, 1.0, 0.5, 100) == pytest.approx(0.5 / 50.0)
+
+
+def _fp16_accumulated(A, B):
+    """C = A B with every partial sum rounded to FP16 (an FP16 accumulator),
+    products formed in FP32: the mistake the FP16-output gate must catch."""
+    acc = np.zeros((A.shape[0], B.shape[1]), dtype=np.float16)
+    for k in range(A.shape[1]):
+        acc = (acc.astype(np.float32) + np.outer(A[:, k], B[k, :]).astype(np.float32)).astype(np.float16)
+    return acc.astype(np.float32)
+
+
+@pytest.mark.parametrize("K", [128, 256])
+def test_fp16_output_gate_rejects_fp16_accumulation_the_reference_gate_accepts(K):
+    """U[-1,1) operands: an FP32-accumulated, once-rounded FP16 C meets the
+    FP16-output gate; a C accumulated in FP16 fails it, although the reference's
+    three gates (1e-2 Frobenius, 5e-2 max element, 1e-3 normalised) accept it."""
+    M, N = 96, 80
+    Ab = O.uniform_fill_f16(M * K, 21).reshape(M, K)
+    Bb = O.uniform_fill_f16(K * N, 22).reshape(K, N)
+    A = O.f16_bits_to_f32(Ab).reshape(M, K)
+    B = O.f16_bits_to_f32(Bb).reshape(K, N)
+    ref = O.gemm_f64(Ab, Bb, M, N, K)
+    absprod = O.gemm_f64(O.abs_bits(Ab), O.abs_bits(Bb), M, N, K)
+    good = (A.astype(np.float32) @ B.astype(np.float32)).astype(np.float16).astype(np.float32)
+    ok, frob, worst = O.passes_fp16(good, ref, absprod, K)
+    assert ok and frob < 4e-4 and worst < 1.0
+    bad = _fp16_accumulated(A, B)
+    assert O.passes(bad, ref, 1.0, 1.0, K)[0]          # the reference's gates accept it
+    ok, frob, worst = O.passes_fp16(bad, ref, absprod, K)
+    assert not ok and frob > 1e-3 and worst > 1.0       # the FP16-output gate does not
+
+
+def test_fp16_output_bound_closed_forms():
+    """The bound is 2^-11 |ref| + (1 + 2^-11) gamma + 2^-25 with gamma =
+    1.001 K 2^-24 |A||B|; a result off by one FP16 half-ulp of ref passes, one
+    off by two full ulps of a normal ref fails."""
+    ref = np.array([[1.0, -3.0, 1000.0]])
+    absprod = np.zeros_like(ref)
+    b = O.fp16_output_bound(ref, absprod, 1)
+    assert np.allclose(b, 2.0 ** -11 * np.abs(ref) + 2.0 ** -25)
+    half_ulp = np.array([[2.0 ** -11, 2.0 ** -10, 0.25]])  # half an FP16 ulp at 1, 3 and 1000
+    assert O.passes_fp16(ref + half_ulp, ref, absprod, 1)[2] <= 1.0
+    two_ulp = np.array([[2.0 ** -9, 0.0, 0.0]])
+    assert O.passes_fp16(ref + two_ulp, ref, absprod, 1)[2] > 1.0
+    g = O.fp16_output_bound(np.zeros((1, 1)), np.array([[4.0]]), 1024)
+    assert g[0, 0] == pytest.approx((1 + 2.0 ** -11) * 1.001 * 1024 * 2.0 ** -24 * 4.0 + 2.0 ** -25)
