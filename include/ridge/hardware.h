@@ -82,6 +82,25 @@ struct HardwareModel {
                                      //    time runs at clockHz x (1 - (1 - loadedClockRatio) u)
     double loadedClockRatio = 0.0;   // [CAL] clock of the ping-pong skeleton with the GEMM's reads
                                      // and refill over that of its MFMAs alone (cal-smem-bw)
+    int hbmWriteModel = 0;           // 0: every DRAM byte, C included, moves at hbmBytesPerSec (reference)
+                                     // 1: C's bytes are written at hbmWriteBytesPerSec and A and B's
+                                     //    read at hbmBytesPerSec; the bus carries one direction at a
+                                     //    time, so the two times add (the epilogue drains at the
+                                     //    write rate too)
+    double hbmWriteBytesPerSec = 0.0;  // [CAL] streaming 16-byte stores, whole GPU (cal-hbm-bw)
+    int fillLatencyModel = 0;        // 0: fill costs only its bytes at the DRAM rate (reference)
+                                     // 1: each round of one-tile-per-workgroup workgroups (one
+                                     //    round in all for a persistent grid) also waits
+                                     //    fillLatencySec before its first matrix instruction
+    double fillLatencySec = 0.0;     // [CAL] a full grid's first-tile load latency (cal-hbm-bw)
+    int mallStreamModel = 0;         // 0: every panel reload is an L2 hit (reference)
+                                     // 1: the first load of a panel on each XCD (the kernels' launch
+                                     //    order) crosses to the MALL; the K-step stretches with the
+                                     //    load that stream puts on the MALL path, read off the
+                                     //    skeleton's calibrated curve
+    double mallRefillBytesPerSec = 0.0;  // [CAL] rate of the L2-missing refill path (cal-smem-bw)
+    double mallStretchLoad[5] = {0.0, 0.0, 0.0, 0.0, 0.0};  // [CAL] path load at miss share 0..1
+    double mallStretch[5] = {0.0, 0.0, 0.0, 0.0, 0.0};      // [CAL] the skeleton K-step's stretch there
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -57,6 +57,12 @@ struct Prediction {
 
     // Power-limited clock (powerModel 1; 1.0 otherwise).
     double powerClockFactor = 1.0;     // clock under this row's load over a pure MFMA stream's
+
+    // First-tile latency (fillLatencyModel 1; 0 otherwise).
+    double fillRounds = 0.0;           // rounds of workgroups that each wait one first-tile latency
+    double refillMissShare = 0.0;      // share of the tile refill that misses the L2 (mallStreamModel 1)
+    double mallLoad = 0.0;             // load that stream puts on the MALL path (mallStreamModel 1)
+    double mallStretch = 1.0;          // K-step stretch read off the calibrated curve (mallStreamModel 1)
 };
 
 }  // namespace ridge

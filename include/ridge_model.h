@@ -44,6 +44,10 @@ typedef struct ridge_model_prediction {
     double tailClockFactor;  /* clock of the last wave over the full-chip clock (clockModel 1) */
     double l2HitBytes;       /* tile-load bytes served by the L2s (l2StreamModel 1) */
     double powerClockFactor; /* clock under this row's load over a pure MFMA stream's (powerModel 1) */
+    double fillRounds;       /* rounds that each wait one first-tile latency (fillLatencyModel 1) */
+    double refillMissShare;  /* share of the tile refill that misses the L2 (mallStreamModel 1) */
+    double mallLoad;         /* load that stream puts on the MALL path (mallStreamModel 1) */
+    double mallStretch;      /* K-step stretch from the calibrated curve (mallStreamModel 1) */
 } ridge_model_prediction_t;
 
 /* Default config (the reference's GemmConfig defaults, config.h:18-39). */

@@ -104,6 +104,14 @@ def band_check(res, spec):
     if "hbmWriteBytesPerSec" in res:
         ok &= check("hbmWriteBytesPerSec", res["hbmWriteBytesPerSec"] / 1e12, spec["hbm_bytes_per_sec"] * 0.40 / 1e12,
                     spec["hbm_bytes_per_sec"] * 1.02 / 1e12, "TB/s", "streaming stores over 4 GiB")
+    if "fillLatencySec" in res:
+        ok &= check("fillLatencySec", res["fillLatencySec"] * 1e6, 0.2, 10.0, "us",
+                    "first-tile wait of a whole grid from HBM")
+    if "mallRefillBytesPerSec" in res:
+        ok &= check("mallRefillBytesPerSec", res["mallRefillBytesPerSec"] / 1e12, 1.0,
+                    res["l2HitBytesPerCycle"] * res["clockHz"] / 1e12, "TB/s",
+                    "L2-missing refill path: below what the L2s serve")
+        ok &= check("mallStretch0", res["mallStretch0"], 0.95, 1.05, "x", "the all-hits skeleton against itself")
     ok &= check("warpsNeededToHide", res["warpsNeededToHide"], 1, 32, "waves/CU")
     # The L2s serve faster than HBM (at the loaded clock); 8 XCDs x 16 channels x
     # 128 B per cycle is the ceiling.
@@ -195,8 +203,16 @@ def hardware_json(res, spec, arch):
     }
     for key in CLOCK_RATIO_KEYS:
         out[key] = res[key]
-    if "hbmWriteBytesPerSec" in res:  # measured by cal-hbm-bw's write sweep
-        out["hbmWriteBytesPerSec"] = res["hbmWriteBytesPerSec"]
+    # Constants of the later calibration benches, written (with the model term
+    # that reads them switched on) when the log has them.
+    for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec"] +
+                ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
+        if key in res:
+            out[key] = res[key]
+    for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]), ("fillLatencyModel", ["fillLatencySec"]),
+                        ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)])):
+        if all(k in res for k in needs):
+            out[term] = 1
     for key in SKELETON_KEYS:
         if key in res:
             out[key] = res[key]

@@ -16,7 +16,8 @@
 // constant is the largest middle value whose repeats are stable.
 //
 // hbmWriteBytesPerSec is the same sweep for 16-byte streaming stores (a GEMM
-// writes its C this way). A 64 MiB buffer (MALL-resident) is also timed and reported as information:
+// writes its C this way). fillLatencySec is the wait of a workgroup's first
+// load when a whole grid starts at once and the data comes from HBM. A 64 MiB buffer (MALL-resident) is also timed and reported as information:
 // that is the level that serves cross-XCD panel re-reads in the GEMM.
 // l2HitBytesPerCycle times the same kind of read (16 GiB of it) with every index
 // wrapped into a 1 MiB buffer, which each XCD's L2 holds, in shader cycles: the
@@ -85,6 +86,23 @@ __global__ __launch_bounds__(kLanes) void streamWriteKernel(float4_t* __restrict
         v[2] += 1.0f;
         p += Flight * stride;
     }
+}
+
+// First-tile latency: every workgroup issues one 16-byte load per lane (1 KiB)
+// the moment it starts, from its own line (`strideChunks` apart, so lines of
+// different workgroups share no DRAM page), waits for the data and records the
+// wait in s_memrealtime ticks (100 MHz). A whole grid starting together is what
+// a GEMM's first K tiles see.
+__global__ __launch_bounds__(64) void firstLoadKernel(const float4_t* __restrict__ src, size_t strideChunks,
+                                                      float* sink, uint64_t* waits) {
+    const uint64_t t0 = realtime();
+    __builtin_amdgcn_sched_barrier(0);
+    const float4_t v = src[size_t(blockIdx.x) * strideChunks + threadIdx.x];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const uint64_t t1 = realtime();
+    if (v[0] == -1.0e38f) sink[0] = v[1];
+    if (threadIdx.x == 0) waits[blockIdx.x] = t1 - t0;
 }
 
 // The same read over `n` float4 positions, each wrapped into the first `mask + 1`
@@ -200,6 +218,35 @@ void printCurve(const char* what, const std::vector<ReadPoint>& curve) {
     }
 }
 
+// Middle first-tile wait (seconds) of `blocks` workgroups over kRepeats
+// launches. Launch r reads the region [r * region, (r + 1) * region) of `src`,
+// region = blocks * stride bytes; with `fresh` those lines have not been read
+// since the caller's earlier sweeps moved other gigabytes through the 256 MiB
+// MALL, so they come from HBM; without it every launch re-reads region 0, which
+// the MALL then holds.
+double firstTileWait(const float4_t* src, size_t bufBytes, int blocks, size_t strideBytes, bool fresh, float* sink,
+                     uint64_t* dWaits, std::vector<double>& reps) {
+    const size_t region = size_t(blocks) * strideBytes;
+    if (size_t(kRepeats + 1) * region > bufBytes) {
+        std::fprintf(stderr, "first-tile regions (%d x %zu bytes) exceed the buffer\n", kRepeats + 1, region);
+        std::exit(2);
+    }
+    reps.clear();
+    std::vector<uint64_t> w(blocks);
+    for (int r = -1; r < kRepeats; ++r) {  // launch -1 is untimed: it brings region 0 in for the warm case
+        const size_t base = fresh ? size_t(r + 1) * region : 0;
+        hipLaunchKernelGGL(firstLoadKernel, dim3(blocks), dim3(64), 0, nullptr, src + base / sizeof(float4_t),
+                           strideBytes / sizeof(float4_t), sink, dWaits);
+        CAL_HIP_CHECK(hipGetLastError());
+        CAL_HIP_CHECK(hipDeviceSynchronize());
+        if (r < 0) continue;
+        CAL_HIP_CHECK(hipMemcpy(w.data(), dWaits, blocks * sizeof(uint64_t), hipMemcpyDeviceToHost));
+        std::vector<double> s(w.begin(), w.end());
+        reps.push_back(middle(s) / kRealtimeHz);
+    }
+    return middle(reps);
+}
+
 template <bool NonTemporal>
 void sweepFlight(std::vector<ReadPoint>& out, float4_t* src, size_t bytes, float* sink, int cus, int wgPerCu) {
     out.push_back(timeRead<1, NonTemporal>(src, bytes, sink, cus, wgPerCu));
@@ -279,6 +326,27 @@ int main() {
                 bestWrite->flight, bestWrite->wgPerCu, bestWrite->nonTemporal ? "non-temporal" : "default");
     const bool writeStable = reportConstant("hbmWriteBytesPerSec", hbmWrite / 1e9, "GB/s", bestWrite->reps);
     CAL_HIP_CHECK(hipMemset(src, 1, kBytes));
+
+    // First-tile latency, one workgroup per CU and two, each from its own line
+    // 256 KiB from the next: from HBM (lines untouched since the memset above
+    // streamed 4 GiB through the MALL) and, for comparison, from the MALL.
+    uint64_t* dWaits = nullptr;
+    CAL_HIP_CHECK(hipMalloc(&dWaits, 2 * cus * sizeof(uint64_t)));
+    std::vector<double> latReps, lat2Reps, mallLatReps;
+    const double fillLatency = firstTileWait(src, kBytes, cus, 256 << 10, true, sink, dWaits, latReps);
+    const double fillLatency2 = firstTileWait(src, kBytes, 2 * cus, 256 << 10, true, sink, dWaits, lat2Reps);
+    const double mallLatency = firstTileWait(src, kBytes, cus, 256 << 10, false, sink, dWaits, mallLatReps);
+    CAL_HIP_CHECK(hipFree(dWaits));
+    std::printf("\nfirst-tile wait: a whole grid starting together, 1 KiB per workgroup from its own line\n");
+    std::printf("  %-40s %8.3f us\n", "one workgroup per CU, from HBM", fillLatency * 1e6);
+    std::printf("  %-40s %8.3f us\n", "two workgroups per CU, from HBM", fillLatency2 * 1e6);
+    std::printf("  %-40s %8.3f us\n", "one workgroup per CU, from the MALL", mallLatency * 1e6);
+    // ~72 ticks of the 100 MHz counter: repeats cannot agree to 5%. The middle
+    // value reproduces (0.72 us on separate boxes); the limit is 25%.
+    const bool latStable = reportConstant("fillLatencySec", fillLatency * 1e6, "us", latReps, 0.25);
+    std::printf("CAL_INFO fillLatencyTwoPerCuSec %.6e\n", fillLatency2);
+    std::printf("CAL_INFO mallLatencySec %.6e\n", mallLatency);
+
     const ReadPoint mallPt = timeRead<4, false>(src, kMallBytes, sink, cus, 8);
     const double mall = mallPt.bytesPerSec;
     std::printf("  %-24s %12.1f GB/s (64 MiB, MALL-resident, information only)\n", "mallBytesPerSec", mall / 1e9);
@@ -301,9 +369,10 @@ int main() {
     CAL_HIP_CHECK(hipFree(dStamps));
     std::printf("\nCAL_RESULT hbmBytesPerSec %.6e\n", hbm);
     std::printf("CAL_RESULT hbmWriteBytesPerSec %.6e\n", hbmWrite);
+    std::printf("CAL_RESULT fillLatencySec %.6e\n", fillLatency);
     std::printf("CAL_RESULT mallBytesPerSec %.6e\n", mall);
     std::printf("CAL_RESULT l2HitBytesPerCycle %.6f\n", l2);
     CAL_HIP_CHECK(hipFree(src));
     CAL_HIP_CHECK(hipFree(sink));
-    return stable && writeStable && l2Stable ? 0 : 1;
+    return stable && writeStable && latStable && l2Stable ? 0 : 1;
 }

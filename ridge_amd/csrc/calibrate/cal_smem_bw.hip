@@ -99,8 +99,18 @@ __global__ __launch_bounds__(Waves * 64) void ldsReadKernel(int iters, uint32_t*
 //   4  every wave reads its fragments and then issues its MFMAs, with no barriers:
 //      the uniform schedule of an 8-wave workgroup, whose two waves per SIMD
 //      overlap their phases only as the hardware interleaves them
+//   5  mode 3 with one of each wave's four refill loads (a quarter of the bytes)
+//      from a window of its own per CU, 512 KiB each: 16 MiB per XCD misses the
+//      4 MiB L2 and 128 MiB in all stays in the 256 MiB MALL
+//   6  mode 3 with all four refill loads from those windows
+//   7  mode 3 with two of the four from those windows
+//   8  mode 3 with three of the four from those windows
 // A perfect overlap makes mode 0 and mode 3 run at max(tC, tS) cycles; the
 // measured clock of each mode shows what the extra data movement costs in power.
+// Modes 3, 5, 7, 8 and 6 (a share m = 0, 1/4, 1/2, 3/4, 1 of the refill missing
+// the L2) give the K-step's stretch against the load m puts on the MALL path: a
+// wave waits for the refill it issued one K-step earlier, the latency budget of
+// the three-stage ping-pong GEMM, whose launch order sets its own share m.
 // Operands are U[-1,1) halves.
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -108,10 +118,11 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 constexpr int kRefillLoads = 4;              // 1 KiB direct-to-LDS loads per wave per phase
 constexpr int kRefillSourceBytes = 1 << 20;  // L2-resident source
 constexpr int kRefillRegion = 48 * 1024;     // refills land in [48 KiB, 64 KiB)
+constexpr int kMallWindowKiB = 512;          // per-CU window of the L2-missing refill
 
 template <int Mode>
-__global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, const char* refill, int iters,
-                                                      float* sink, Stamp* out) {
+__global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, const char* refill,
+                                                      const char* mall, int iters, float* sink, Stamp* out) {
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     // 48 KiB of tiles from the 16 KiB operand block, repeated.
     for (int i = threadIdx.x; i < 48 * 1024 / 4; i += blockDim.x)
@@ -141,11 +152,19 @@ __global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, 
     };
     // Load i of wave w at step it reads 1 KiB at ((it * 8 + w) * 4 + i) mod 1024
     // KiB of the source and writes LDS [48 KiB + ((w % 4) * 4 + i) KiB, +1 KiB).
+    // In modes 5 and 6 the first one (or all four) of those loads instead read
+    // 1 KiB at ((it * 8 + w) * 4 + i) mod 512 KiB of this CU's own window of
+    // `mall` (the window of workgroup g starts at g * 512 KiB).
+    const uint32_t window = blockIdx.x * (kMallWindowKiB << 10);
     auto refillLoads = [&](int it) {
 #pragma unroll
         for (int i = 0; i < kRefillLoads; ++i) {
-            const uint32_t off = (uint32_t)(((((it * 8 + wave) * kRefillLoads + i) & 1023) << 10) + lane * 16);
-            ridge::globalLoadLds16(refill, off, ldsBase + kRefillRegion + ((wave % 4) * kRefillLoads + i) * 1024);
+            const uint32_t k = (uint32_t)((it * 8 + wave) * kRefillLoads + i);
+            const uint32_t dst = ldsBase + kRefillRegion + ((wave % 4) * kRefillLoads + i) * 1024;
+            if (i < (Mode == 5 ? 1 : Mode == 7 ? 2 : Mode == 8 ? 3 : Mode == 6 ? 4 : 0))
+                ridge::globalLoadLds16(mall, window + ((k % kMallWindowKiB) << 10) + lane * 16, dst);
+            else
+                ridge::globalLoadLds16(refill, ((k & 1023) << 10) + lane * 16, dst);
         }
     };
     float4_t acc[32];
@@ -155,16 +174,17 @@ __global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, 
         for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;
     __syncthreads();
     readFrags();
-    constexpr bool kPingPong = Mode == 0 || Mode == 3;
+    constexpr bool kRefill = Mode == 3 || Mode >= 5;
+    constexpr bool kPingPong = Mode == 0 || kRefill;
     const uint64_t c0 = cycles();
     const uint64_t r0 = realtime();
     if (kPingPong && group == 1) __builtin_amdgcn_s_barrier();
     for (int it = 0; it < iters; ++it) {
         if (Mode != 2) {  // modes 0, 1, 3, 4 read
-            if (Mode == 3) refillLoads(it);
+            if (kRefill) refillLoads(it);
             readFrags();
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (Mode == 3) ridge::waitVmcnt<kRefillLoads>();  // the previous phase's refill has landed
+            if (kRefill) ridge::waitVmcnt<kRefillLoads>();  // the previous phase's refill has landed
             if (Mode == 1) {
                 // Consume every fragment register, at no instruction cost.
 #pragma unroll
@@ -183,7 +203,7 @@ __global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, 
         }
         if (kPingPong) __builtin_amdgcn_s_barrier();
     }
-    if (Mode == 3) ridge::waitVmcnt<0>();
+    if (kRefill) ridge::waitVmcnt<0>();
     if (kPingPong && group == 0) __builtin_amdgcn_s_barrier();  // both groups pass 2 * iters + 1 barriers
     __syncthreads();
     const uint64_t c1 = cycles();
@@ -198,11 +218,11 @@ __global__ __launch_bounds__(512) void pingPongKernel(const uint32_t* operands, 
 // Median cycles per K-step of the skeleton in `Mode` over every CU, and the
 // median loaded clock.
 template <int Mode>
-double pingPongCycles(int cus, const uint32_t* dOperands, const char* dRefill, float* dSink, Stamp* dStamps,
-                      double& clockHz) {
+double pingPongCycles(int cus, const uint32_t* dOperands, const char* dRefill, const char* dMall, float* dSink,
+                      Stamp* dStamps, double& clockHz) {
     auto k = pingPongKernel<Mode>;
     CAL_HIP_CHECK(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, kOneWorkgroupLds));
-    hipLaunchKernelGGL(k, dim3(cus), dim3(512), kOneWorkgroupLds, nullptr, dOperands, dRefill, kIters, dSink,
+    hipLaunchKernelGGL(k, dim3(cus), dim3(512), kOneWorkgroupLds, nullptr, dOperands, dRefill, dMall, kIters, dSink,
                        dStamps);
     CAL_HIP_CHECK(hipGetLastError());
     CAL_HIP_CHECK(hipDeviceSynchronize());
@@ -321,32 +341,68 @@ int main() {
     CAL_HIP_CHECK(hipMalloc(&dFSink, sizeof(float)));
     CAL_HIP_CHECK(hipMemcpy(dOperands, hOperands.data(), hOperands.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
     CAL_HIP_CHECK(hipMemset(dRefill, 0x3c, kRefillSourceBytes));
-    std::vector<double> st[5], hz[5];
+    // The L2-missing windows: one per CU (workgroup g uses [g * 512 KiB, +512 KiB)).
+    char* dMall = nullptr;
+    const size_t mallBytes = size_t(cus) * (kMallWindowKiB << 10);
+    CAL_HIP_CHECK(hipMalloc(&dMall, mallBytes));
+    CAL_HIP_CHECK(hipMemset(dMall, 0x3c, mallBytes));
+    constexpr int kModes = 9;
+    std::vector<double> st[kModes], hz[kModes];
     for (int r = 0; r < kRepeats; ++r) {
         double h = 0.0;
-        st[0].push_back(pingPongCycles<0>(cus, dOperands, dRefill, dFSink, dStamps, h));
-        hz[0].push_back(h);
-        st[1].push_back(pingPongCycles<1>(cus, dOperands, dRefill, dFSink, dStamps, h));
-        hz[1].push_back(h);
-        st[2].push_back(pingPongCycles<2>(cus, dOperands, dRefill, dFSink, dStamps, h));
-        hz[2].push_back(h);
-        st[3].push_back(pingPongCycles<3>(cus, dOperands, dRefill, dFSink, dStamps, h));
-        hz[3].push_back(h);
-        st[4].push_back(pingPongCycles<4>(cus, dOperands, dRefill, dFSink, dStamps, h));
-        hz[4].push_back(h);
+#define CAL_MODE(M)                                                                             \
+    st[M].push_back(pingPongCycles<M>(cus, dOperands, dRefill, dMall, dFSink, dStamps, h));    \
+    hz[M].push_back(h)
+        CAL_MODE(0);
+        CAL_MODE(1);
+        CAL_MODE(2);
+        CAL_MODE(3);
+        CAL_MODE(4);
+        CAL_MODE(5);
+        CAL_MODE(6);
+        CAL_MODE(7);
+        CAL_MODE(8);
+#undef CAL_MODE
     }
-    const char* kModeNames[5] = {"ping-pong (reads under MFMAs)", "fragment reads alone", "MFMAs alone",
-                                 "ping-pong + 32 KiB direct-to-LDS refill", "free-running (no barriers)"};
-    const char* kModeKeys[5] = {"pingPongStepCycles", "pingPongReadCycles", "pingPongMfmaCycles",
-                                "pingPongRefillStepCycles", "freeRunningStepCycles"};
+    const char* kModeNames[kModes] = {"ping-pong (reads under MFMAs)", "fragment reads alone", "MFMAs alone",
+                                      "ping-pong + 32 KiB direct-to-LDS refill", "free-running (no barriers)",
+                                      "the refill, 1/4 missing the L2", "the refill, all missing the L2",
+                                      "the refill, 1/2 missing the L2", "the refill, 3/4 missing the L2"};
+    const char* kModeKeys[kModes] = {"pingPongStepCycles", "pingPongReadCycles", "pingPongMfmaCycles",
+                                     "pingPongRefillStepCycles", "freeRunningStepCycles",
+                                     "pingPongMiss25StepCycles", "pingPongMiss100StepCycles",
+                                     "pingPongMiss50StepCycles", "pingPongMiss75StepCycles"};
     std::printf("\nping-pong skeleton: 8 waves (2 per SIMD), 128x64 wavefront tiles, BK = 32; per K-step per CU\n");
-    double tStep[5];
-    for (int m = 0; m < 5; ++m) {
+    double tStep[kModes], clock[kModes];
+    for (int m = 0; m < kModes; ++m) {
         tStep[m] = middle(st[m]);
-        std::printf("  %-44s %8.1f cycles  %7.1f MHz\n", kModeNames[m], tStep[m], middle(hz[m]) / 1e6);
+        clock[m] = middle(hz[m]);
+        std::printf("  %-44s %8.1f cycles  %7.1f MHz\n", kModeNames[m], tStep[m], clock[m] / 1e6);
         std::printf("CAL_INFO %s %.6f\n", kModeKeys[m], tStep[m]);
-        std::printf("CAL_INFO %sClockHz %.6e\n", kModeKeys[m], middle(hz[m]));
+        std::printf("CAL_INFO %sClockHz %.6e\n", kModeKeys[m], clock[m]);
     }
+    // The L2-missing refill path. With all of the refill missing the L2 the
+    // K-step is bound by that path (it stretches to its transfer time), which
+    // gives the path's rate; a share m of the refill then loads the path to
+    // rho = m x (its all-miss transfer time) / (the all-hits K-step time), and
+    // the K-step stretches by t(m) / t(0).
+    const double refillBytes = 32.0 * 1024.0 * cus;  // per K-step, whole chip
+    const double mallRate = refillBytes / (tStep[6] / clock[6]);
+    const double allMissLoad = (tStep[6] / clock[6]) / (tStep[3] / clock[3]);
+    std::printf("  L2-missing refill path: %.2f TB/s (the all-miss K-step is bound by it)\n", mallRate / 1e12);
+    std::printf("CAL_RESULT mallRefillBytesPerSec %.6e\n", mallRate);
+    const int curveModes[5] = {3, 5, 7, 8, 6};
+    const double shares[5] = {0.0, 0.25, 0.5, 0.75, 1.0};
+    std::printf("  %8s %8s %12s %10s\n", "miss", "load", "stretch", "clock");
+    for (int i = 0; i < 5; ++i) {
+        const int m = curveModes[i];
+        const double load = shares[i] * allMissLoad;
+        const double stretch = (tStep[m] / clock[m]) / (tStep[3] / clock[3]);
+        std::printf("  %8.2f %8.3f %12.4f %10.4f\n", shares[i], load, stretch, clock[m] / clock[3]);
+        std::printf("CAL_RESULT mallStretchLoad%d %.6f\n", i, load);
+        std::printf("CAL_RESULT mallStretch%d %.6f\n", i, stretch);
+    }
+    CAL_HIP_CHECK(hipFree(dMall));
     const double tS = 8 * (8 * 1024.0 / a.best + 8 * 512.0 / b.best);
     std::printf("  reads alone against the per-operand rates: %.1f measured, %.1f from ldsA/ldsBTr\n", tStep[1], tS);
     std::printf("  cost of a phase switch: %.1f cycles ((ping-pong - max(reads, MFMAs)) / 2)\n",
@@ -358,7 +414,10 @@ int main() {
         (tStep[1] + tStep[2] - tStep[4]) / std::min(tStep[1], tStep[2]);
     std::printf("  free-running waves hide %.3f of the shorter phase under the longer\n", hidden);
     std::printf("CAL_RESULT freeRunningOverlap %.6f\n", hidden);
-    for (int m = 0; m < 5; ++m) ok &= reportConstant(kModeKeys[m], tStep[m], "cycles", st[m]);
+    // Modes bound by the L2-missing path (3/4 and all of the refill missing)
+    // queue on it and spread more from launch to launch; their limit is 20%.
+    for (int m = 0; m < kModes; ++m)
+        ok &= reportConstant(kModeKeys[m], tStep[m], "cycles", st[m], (m == 6 || m == 8) ? 0.20 : 0.05);
     CAL_HIP_CHECK(hipFree(dOperands));
     CAL_HIP_CHECK(hipFree(dRefill));
     CAL_HIP_CHECK(hipFree(dFSink));

@@ -111,6 +111,14 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("l2HitBytesPerCycle", h.l2HitBytesPerCycle), I("uniformOverlapModel", h.uniformOverlapModel),
         R("freeRunningOverlap", h.freeRunningOverlap), I("powerModel", h.powerModel),
         R("loadedClockRatio", h.loadedClockRatio), R("warpsNeededToHideIlp8", h.warpsNeededToHideIlp8),
+        I("hbmWriteModel", h.hbmWriteModel), R("hbmWriteBytesPerSec", h.hbmWriteBytesPerSec),
+        I("fillLatencyModel", h.fillLatencyModel), R("fillLatencySec", h.fillLatencySec),
+        I("mallStreamModel", h.mallStreamModel), R("mallRefillBytesPerSec", h.mallRefillBytesPerSec),
+        R("mallStretchLoad0", h.mallStretchLoad[0]), R("mallStretchLoad1", h.mallStretchLoad[1]),
+        R("mallStretchLoad2", h.mallStretchLoad[2]), R("mallStretchLoad3", h.mallStretchLoad[3]),
+        R("mallStretchLoad4", h.mallStretchLoad[4]), R("mallStretch0", h.mallStretch[0]),
+        R("mallStretch1", h.mallStretch[1]), R("mallStretch2", h.mallStretch[2]), R("mallStretch3", h.mallStretch[3]),
+        R("mallStretch4", h.mallStretch[4]),
     };
 }
 
@@ -157,6 +165,18 @@ std::string inconsistency(const HardwareModel& h) {
         return "uniformOverlapModel 1 reads freeRunningOverlap, which must lie in [0, 1]";
     if (h.powerModel == 1 && !(h.loadedClockRatio > 0.0 && h.loadedClockRatio <= 1.0))
         return "powerModel 1 reads loadedClockRatio, which must lie in (0, 1]";
+    if (h.mallStreamModel == 1) {
+        bool rising = h.mallRefillBytesPerSec > 0.0 && h.mallStretchLoad[0] >= 0.0;
+        for (int i = 0; i < 4; ++i) rising = rising && h.mallStretchLoad[i + 1] > h.mallStretchLoad[i];
+        for (int i = 0; i < 5; ++i) rising = rising && h.mallStretch[i] > 0.0;
+        if (!rising)
+            return "mallStreamModel 1 reads mallRefillBytesPerSec (positive) and the mallStretchLoad0..4 / "
+                   "mallStretch0..4 curve (loads increasing, stretches positive)";
+    }
+    if (h.hbmWriteModel == 1 && !(h.hbmWriteBytesPerSec > 0.0))
+        return "hbmWriteModel 1 reads hbmWriteBytesPerSec, which must be positive";
+    if (h.fillLatencyModel == 1 && !(h.fillLatencySec > 0.0))
+        return "fillLatencyModel 1 reads fillLatencySec, which must be positive";
     return "";
 }
 

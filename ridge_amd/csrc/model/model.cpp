@@ -39,9 +39,19 @@
 //   power-limited clock   = hw.powerModel 1: the clock falls with the share of
 //                           time the matrix pipes are busy, to loadedClockRatio
 //                           when they always are (reference: one clock)
+//   MALL stream           = hw.mallStreamModel 1: the K-step stretches with the
+//                           load the launch order's L2-missing refill puts on
+//                           the MALL path, as a calibrated skeleton's does
+//                           (reference: the L2 serves every panel)
+//   first-tile latency    = hw.fillLatencyModel 1: each round of workgroups waits
+//                           one measured DRAM latency for its first tile
+//                           (reference: the fill costs only bandwidth)
 //   L2 stream             = hw.l2StreamModel 1: tile loads the L2s serve take
 //                           their own time, in series with the HBM stream
 //                           (reference: the HBM roofline alone)
+//   write stream          = hw.hbmWriteModel 1: C is written at the calibrated
+//                           streaming-write rate, A and B read at the read rate,
+//                           and the two times add (reference: one DRAM rate)
 //   persistent rows       = hw.persistentModel 1 and cfg.schedule 2: two loader
 //                           waves and the epilogue staging join the workgroup,
 //                           which walks ceil(tiles / slots) tiles and pays one
@@ -132,6 +142,45 @@ double clockRatioAtBusyShare(const HardwareModel& hw, double busy) {
     return pts[i] + (pts[i + 1] - pts[i]) * f;
 }
 
+// Distinct A row panels and B column panels that the first n workgroups touch,
+// summed over XCDs, in the kernels' exact launch order: hardware workgroup p runs
+// on XCD p % X; the kernel maps it to logical id xcdRemap(p) = x*q + min(x, r) +
+// p / X (q, r = tiles / X, % X), and the logical id to a tile by the GroupM
+// order. XCD x holds the first ceil((n - x) / X) ids of its range, and fetches
+// every distinct panel of its tiles once into its own L2.
+void launchOrderPanels(const GemmConfig& cfg, const HardwareModel& hw, long long n, double& rowPanels,
+                       double& colPanels) {
+    const long long numPidM = cfg.M / cfg.BM;
+    const long long numPidN = cfg.N / cfg.BN;
+    const long long total = numPidM * numPidN;
+    const long long X = hw.numXcds;
+    const long long q = total / X, r = total % X;
+    const long long G = std::max(1, cfg.groupM);
+    std::vector<long long> rowSeen(numPidM, -1), colSeen(numPidN, -1);
+    rowPanels = 0.0;
+    colPanels = 0.0;
+    for (long long x = 0; x < X && x < n; ++x) {
+        const long long base = x * q + std::min(x, r);
+        const long long count = (n - x + X - 1) / X;
+        for (long long j = 0; j < count; ++j) {
+            const long long pid = base + j;
+            const long long pidInGroup = pid % (G * numPidN);
+            const long long firstPidM = (pid / (G * numPidN)) * G;
+            const long long groupRows = std::min(numPidM - firstPidM, G);
+            const long long row = firstPidM + pidInGroup % groupRows;
+            const long long col = pidInGroup / groupRows;
+            if (rowSeen[row] != x) {
+                rowSeen[row] = x;
+                rowPanels += 1.0;
+            }
+            if (colSeen[col] != x) {
+                colSeen[col] = x;
+                colPanels += 1.0;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
@@ -174,17 +223,17 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const bool derivedPingPong = hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM && cfg.stages >= 3;
     const bool pingPong = hw.pingPongModel == 1 && (cfg.schedule < 0 ? derivedPingPong : cfg.schedule == 1);
     double tStep = pingPong ? std::max(tCompute, tSmem) : tCompute + tSmem;
-    // uniformOverlapModel 1: the two waves per SIMD of an 8-wave uniform workgroup
-    // hide part of the shorter phase under the longer with no schedule doing it:
-    // the share cal-smem-bw measures for the same waves without barriers.
-    if (!pingPong && hw.uniformOverlapModel == 1 && !persistent && hw.simdsPerSM > 0 &&
-        numWarps == 2 * hw.simdsPerSM)
+    // uniformOverlapModel 1: two compute waves per SIMD that run the uniform
+    // schedule (the 8-wave uniform rows, and the 8-compute-wave persistent rows,
+    // whose compute waves run the same loop with one barrier per K tile) hide
+    // part of the shorter phase under the longer with no schedule doing it: the
+    // share cal-smem-bw measures for the same waves without barriers.
+    if (!pingPong && hw.uniformOverlapModel == 1 && hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM)
         tStep -= hw.freeRunningOverlap * std::min(tCompute, tSmem);
-    const double smEfficiency = tCompute / tStep;
     p.tComputeCycles = tCompute;
     p.tSmemCycles = tSmem;
     p.tStepCycles = tStep;
-    p.smEfficiency = smEfficiency;
+    p.smEfficiency = tCompute / tStep;
 
     // Occupancy: the tightest of LDS, wave slots, registers and the workgroup cap.
     const double ringBytes = double(cfg.stages) * (cfg.BM * cfg.BK + cfg.BK * cfg.BN) * db;
@@ -201,6 +250,41 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         return p;
     }
     p.ctasPerSM = int(ctasPerSM);
+
+    // mallStreamModel 1: the refill of the panels an XCD's resident tiles share
+    // is served by its L2 after the first load; the first loads (distinct panels
+    // per XCD, in the kernels' launch order) cross to the MALL. When that stream
+    // loads the MALL path, a K-step stretches as the calibrated skeleton's did
+    // at the same load (linear between its points, proportional to the load
+    // beyond the last, where the path's bandwidth binds).
+    if (hw.mallStreamModel == 1 && hw.simdsPerSM > 0) {
+        const double slots = ctasPerSM * double(hw.numSMs);
+        const double tiles = double((cfg.M / cfg.BM) * (cfg.N / cfg.BN));
+        const long long n = (long long)std::min(slots, tiles);
+        double rowPanels = 0.0, colPanels = 0.0;
+        launchOrderPanels(cfg, hw, n, rowPanels, colPanels);
+        p.refillMissShare = std::min(1.0, (rowPanels * cfg.BM + colPanels * cfg.BN) / (double(n) * (cfg.BM + cfg.BN)));
+        // Every resident tile advances one K-step per ctasPerSM x tStep cycles of its CU.
+        const double missBytes = (rowPanels * cfg.BM + colPanels * cfg.BN) * double(cfg.BK) * db;
+        const double stepSeconds = ctasPerSM * tStep / hw.clockHz;
+        const double load = missBytes / hw.mallRefillBytesPerSec / stepSeconds;
+        const double* x = hw.mallStretchLoad;
+        const double* y = hw.mallStretch;
+        double stretch = 1.0;
+        if (load >= x[4]) {
+            stretch = y[4] * load / x[4];
+        } else {
+            for (int i = 0; i < 4; ++i)
+                if (load >= x[i] && load <= x[i + 1])
+                    stretch = y[i] + (y[i + 1] - y[i]) * (load - x[i]) / (x[i + 1] - x[i]);
+        }
+        p.mallLoad = load;
+        p.mallStretch = std::max(1.0, stretch);
+        tStep *= p.mallStretch;
+        p.tStepCycles = tStep;
+        p.smEfficiency = tCompute / tStep;
+    }
+    const double smEfficiency = p.smEfficiency;
 
     // Latency hiding: resident waves against the calibrated need. A wave that
     // carries 8 or more independent accumulator chains per K-step hides latency
@@ -246,7 +330,10 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const double prologueTiles =
         hw.prologueModel == 1 ? std::min(double(cfg.stages - 1), kSteps) : double(cfg.stages - 1);
     const double tPrologue = prologueTiles * tileBytes / gmemBytesPerCycle / ctasPerSM;
-    const double tEpilogue = double(cfg.BM) * cfg.BN * double(hw.cBytes) / gmemBytesPerCycle / ctasPerSM;
+    // hbmWriteModel 1: the drain moves at the streaming-write rate.
+    const double drainBytesPerCycle =
+        hw.hbmWriteModel == 1 ? hw.hbmWriteBytesPerSec / (hw.clockHz * double(hw.numSMs)) : gmemBytesPerCycle;
+    const double tEpilogue = double(cfg.BM) * cfg.BN * double(hw.cBytes) / drainBytesPerCycle / ctasPerSM;
     const double tBody = kSteps * tStep;
     double envelopeEfficiency;
     if (persistent) {
@@ -285,54 +372,28 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const double flopsPerCta = 2.0 * double(cfg.BM) * cfg.BN * cfg.K;
     const double baseIntensity = flopsPerCta / globalBytesPerCta;
     double arithmeticIntensity;
+    double panelIntensity;  // FLOP per byte of A and B panel traffic, before the compulsory cap
     if (hw.l2ReuseModel == 0) {
         // Square reuse over all resident slots (reference :116-123).
         const double l2ReuseFactor = std::sqrt(ctaSlots);
         arithmeticIntensity = baseIntensity * l2ReuseFactor;
+        panelIntensity = arithmeticIntensity;
         p.l2ReuseFactor = l2ReuseFactor;
     } else if (hw.l2ReuseModel == 2) {
-        // The kernels' launch order, exactly. Hardware workgroup p runs on XCD
-        // p % X; the kernel maps it to logical id xcdRemap(p) = x*q + min(x, r) +
-        // p / X (q, r = totalCtas / X, % X), and the logical id to a tile by the
-        // GroupM order. The first n = min(slots, tiles) workgroups are resident
-        // together; XCD x holds the first ceil((n - x) / X) ids of its range. Each
-        // XCD fetches every distinct A row panel and B column panel of its
-        // resident tiles once into its own L2; the traffic is summed over XCDs.
-        const long long numPidM = cfg.M / cfg.BM;
-        const long long numPidN = cfg.N / cfg.BN;
-        const long long total = numPidM * numPidN;
+        // The kernels' launch order, exactly (launchOrderPanels): each XCD
+        // fetches every distinct A row panel and B column panel of its resident
+        // tiles once into its own L2; the traffic is summed over XCDs.
         const long long n = (long long)std::min(ctaSlots, totalCtas);
         const long long X = hw.numXcds;
-        const long long q = total / X, r = total % X;
-        const long long G = std::max(1, cfg.groupM);
-        std::vector<long long> rowSeen(numPidM, -1), colSeen(numPidN, -1);
         double rowPanels = 0.0, colPanels = 0.0;
-        for (long long x = 0; x < X && x < n; ++x) {
-            const long long base = x * q + std::min(x, r);
-            const long long count = (n - x + X - 1) / X;
-            for (long long j = 0; j < count; ++j) {
-                const long long pid = base + j;
-                const long long pidInGroup = pid % (G * numPidN);
-                const long long firstPidM = (pid / (G * numPidN)) * G;
-                const long long groupRows = std::min(numPidM - firstPidM, G);
-                const long long row = firstPidM + pidInGroup % groupRows;
-                const long long col = pidInGroup / groupRows;
-                if (rowSeen[row] != x) {
-                    rowSeen[row] = x;
-                    rowPanels += 1.0;
-                }
-                if (colSeen[col] != x) {
-                    colSeen[col] = x;
-                    colPanels += 1.0;
-                }
-            }
-        }
+        launchOrderPanels(cfg, hw, n, rowPanels, colPanels);
         const double residentFlops = 2.0 * double(n) * cfg.BM * cfg.BN * double(cfg.K);
         const double residentBytes = (rowPanels * cfg.BM + colPanels * cfg.BN) * double(cfg.K) * db;
         const double l2Intensity = residentFlops / residentBytes;
         const double M = double(cfg.M), N = double(cfg.N), K = double(cfg.K);
         const double compulsory = 2.0 * M * N * K / ((M * K + K * N) * db + M * N * hw.cBytes);
         arithmeticIntensity = std::min(l2Intensity, compulsory);
+        panelIntensity = l2Intensity;
         p.l2ReuseFactor = arithmeticIntensity / baseIntensity;
         const double xcdsUsed = double(std::min(X, n));
         p.reuseTilesM = rowPanels / xcdsUsed;
@@ -357,6 +418,7 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         const double M = double(cfg.M), N = double(cfg.N), K = double(cfg.K);
         const double compulsory = 2.0 * M * N * K / ((M * K + K * N) * db + M * N * hw.cBytes);
         arithmeticIntensity = std::min(l2Intensity, compulsory);
+        panelIntensity = l2Intensity;
         p.l2ReuseFactor = arithmeticIntensity / baseIntensity;
         p.reuseTilesM = a;
         p.reuseTilesN = b;
@@ -365,7 +427,23 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     p.baseIntensity = baseIntensity;
     p.arithmeticIntensity = arithmeticIntensity;
     p.hbmTFLOPS = hw.hbmBytesPerSec * arithmeticIntensity / 1e12;
-    if (hw.l2StreamModel == 1) {
+    if (hw.hbmWriteModel == 1) {
+        // DRAM traffic split by direction: A and B panels (at least once each)
+        // read at the read rate, C written once at the write rate, one after the
+        // other on the bus. With l2StreamModel 1 the panel loads that the L2s
+        // serve take their own time on top, as below.
+        const double M = double(cfg.M), N = double(cfg.N), K = double(cfg.K);
+        const double flops = 2.0 * M * N * K;
+        const double readBytes = std::max(flops / panelIntensity, (M * K + K * N) * db);
+        const double writeBytes = M * N * hw.cBytes;
+        double seconds = readBytes / hw.hbmBytesPerSec + writeBytes / hw.hbmWriteBytesPerSec;
+        if (hw.l2StreamModel == 1) {
+            p.l2HitBytes = std::max(0.0, flops / baseIntensity - readBytes);
+            seconds += p.l2HitBytes / (hw.l2HitBytesPerCycle * hw.clockHz);
+        }
+        p.arithmeticIntensity = flops / (readBytes + writeBytes);
+        p.hbmTFLOPS = flops / seconds / 1e12;
+    } else if (hw.l2StreamModel == 1) {
         // Every workgroup loads its (BM + BN) x K panels; the share that HBM does
         // not supply (a panel re-read by the workgroups of one XCD) is served by
         // that XCD's L2, and a load-only kernel with the GEMM's streams takes the
@@ -381,6 +459,20 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
 
     // The label names the derating furthest from 1.0 (reference :129-143).
     p.predictedTFLOPS = std::min(computeTFLOPS, p.hbmTFLOPS);
+    if (hw.fillLatencyModel == 1) {
+        // A workgroup's first K tile cannot be fetched before the workgroup
+        // exists, so every round of one-tile-per-workgroup workgroups waits one
+        // loaded DRAM latency before its first MFMA; a persistent grid waits
+        // once. The wait adds to whichever ceiling binds, so it is added to both.
+        const double rounds = persistent ? 1.0 : fullWaves;
+        const double flops = 2.0 * double(cfg.M) * double(cfg.N) * double(cfg.K);
+        const double wait = rounds * hw.fillLatencySec;
+        computeTFLOPS = flops / (flops / (computeTFLOPS * 1e12) + wait) / 1e12;
+        p.hbmTFLOPS = flops / (flops / (p.hbmTFLOPS * 1e12) + wait) / 1e12;
+        p.computeTFLOPS = computeTFLOPS;
+        p.fillRounds = rounds;
+        p.predictedTFLOPS = std::min(computeTFLOPS, p.hbmTFLOPS);
+    }
     if (p.hbmTFLOPS < computeTFLOPS) {
         p.bottleneck = Bottleneck::Hbm;
     } else {

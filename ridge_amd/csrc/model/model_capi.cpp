@@ -129,6 +129,10 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     out->tailClockFactor = p.tailClockFactor;
     out->l2HitBytes = p.l2HitBytes;
     out->powerClockFactor = p.powerClockFactor;
+    out->fillRounds = p.fillRounds;
+    out->refillMissShare = p.refillMissShare;
+    out->mallLoad = p.mallLoad;
+    out->mallStretch = p.mallStretch;
     return 0;
 }
 

@@ -32,7 +32,8 @@ _PRED_FIELDS = [("predictedTFLOPS", ctypes.c_double), ("bottleneck", ctypes.c_in
                                     "tPrologueCycles", "tEpilogueCycles", "tBodyCycles", "kSteps")] + \
     [("numWarps", ctypes.c_int), ("ctasPerSM", ctypes.c_int)] + \
     [(n, ctypes.c_double) for n in ("tComputeCycles", "tSmemCycles", "tStepCycles", "reuseTilesM", "reuseTilesN",
-                                    "compulsoryIntensity", "tailClockFactor", "l2HitBytes", "powerClockFactor")]
+                                    "compulsoryIntensity", "tailClockFactor", "l2HitBytes", "powerClockFactor",
+                                    "fillRounds", "refillMissShare", "mallLoad", "mallStretch")]
 
 
 class _Prediction(ctypes.Structure):

@@ -119,5 +119,7 @@ def test_binding_struct_layouts_match_the_libraries():
     L = RM.lib()
     assert L.ridge_model_config_size() == ctypes.sizeof(RM._Config)
     assert L.ridge_model_prediction_size() == ctypes.sizeof(RM._Prediction)
-    # The prediction ends with the two gfx950 fields, after the reference's.
-    assert [f for f, _ in RM._Prediction._fields_][-3:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor"]
+    # The prediction ends with the gfx950 fields, after the reference's.
+    assert [f for f, _ in RM._Prediction._fields_][-7:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor",
+                                                            "fillRounds", "refillMissShare", "mallLoad",
+                                                            "mallStretch"]

@@ -525,7 +525,8 @@ def test_uniform_overlap_model_hides_part_of_the_shorter_phase(tmp_path):
     (4 cycles per MFMA per CU, 128 B/cycle LDS): the 8-wave uniform 256x256x32
     w128x64 tile at 2 stages has tC = 1024, tS = 768 and runs
     1024 + 768 - 0.75 x 768 = 1216 cycles per K-step (in series: 1792). A 4-wave
-    uniform workgroup (one wave per SIMD) and the ping-pong rows are unchanged."""
+    uniform workgroup (one wave per SIMD) and the ping-pong rows are unchanged;
+    the 8-compute-wave persistent row is covered."""
     on = tmp_path / "on.json"
     on.write_text(_CDNA4_JSON % ', "uniformOverlapModel": 1, "freeRunningOverlap": 0.75')
     off = tmp_path / "off.json"
@@ -538,7 +539,106 @@ def test_uniform_overlap_model_hides_part_of_the_shorter_phase(tmp_path):
     assert RM.predict(hw_on, **four)["tStepCycles"] == RM.predict(hw_off, **four)["tStepCycles"]
     pp = dict(eight, stages=4)
     assert RM.predict(hw_on, **pp)["tStepCycles"] == pytest.approx(1024.0)
+    # The 8-compute-wave persistent row (256x128x32 w64x64, schedule 2): its
+    # compute waves run the same uniform loop, two per SIMD: tC = 16 MFMAs x 8
+    # waves x 4 = 512, tS = 8 x (64 + 64) x 32 x 2 B / 128 = 512, so
+    # 512 + 512 - 0.75 x 512 = 640 cycles (in series: 1024).
+    pers = dict(M=8192, N=8192, K=128, BM=256, BN=128, BK=32, warpM=64, warpN=64, stages=6, regsPerThread=167,
+                groupM=4, schedule=2)
+    assert RM.predict(hw_off, **pers)["tStepCycles"] == pytest.approx(1024.0)
+    assert RM.predict(hw_on, **pers)["tStepCycles"] == pytest.approx(640.0)
     bad = tmp_path / "bad.json"
     bad.write_text(_CDNA4_JSON % ', "uniformOverlapModel": 1, "freeRunningOverlap": 1.5')
     with pytest.raises(ValueError, match="uniformOverlapModel 1"):
         RM.Hardware(str(bad))
+
+
+def test_mall_stream_model_stretches_the_k_step_with_launch_order_misses(tmp_path):
+    """mallStreamModel 1 on the placeholders (4 cycles per MFMA, 128 B/cycle LDS,
+    2.4 GHz), MALL path 8 TB/s, stretch curve (load: stretch) 0: 1, 0.5: 1,
+    1.0: 1.1, 1.5: 1.5, 2.0: 2.0. 8192 x 8192 x 4096, 256x256x32 w128x64 s4
+    ping-pong, one workgroup per CU: tC = 32 MFMAs x 8 waves x 4 = 1024 cycles,
+    tS = 8 x 192 x 64 / 128 = 768, K-step max = 1024 cycles = 426.67 ns.
+    256 tiles resident, 32 per XCD (XCD x holds logical ids 128x .. 128x+31):
+      groupM 1: one tile row, 32 columns: 1 + 32 panels per XCD, 8 + 256 in all;
+        misses per K-step (8 x 256 + 256 x 256) x 32 x 2 B = 4,325,376 B,
+        load 4,325,376 / 8e12 / 426.67 ns = 1.26720, stretch 1.1 + 0.4 x
+        0.2672 / 0.5 = 1.31376, miss share 67,584 / (256 x 512) = 0.515625;
+      groupM 4: 4 rows x 8 columns: 32 + 64 panels in all: 1,572,864 B,
+        load 0.46080, stretch 1, miss share 0.1875."""
+    curve = (', "mallStreamModel": 1, "mallRefillBytesPerSec": 8e12, '
+             '"mallStretchLoad0": 0, "mallStretchLoad1": 0.5, "mallStretchLoad2": 1.0, "mallStretchLoad3": 1.5, '
+             '"mallStretchLoad4": 2.0, "mallStretch0": 1, "mallStretch1": 1, "mallStretch2": 1.1, '
+             '"mallStretch3": 1.5, "mallStretch4": 2.0')
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % curve)
+    hw = RM.Hardware(str(on))
+    cfg = dict(M=8192, N=8192, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=4, regsPerThread=197,
+               schedule=1)
+    g1 = RM.predict(hw, groupM=1, **cfg)
+    assert g1["refillMissShare"] == pytest.approx(0.515625)
+    assert g1["mallLoad"] == pytest.approx(4325376 / 8e12 / (1024 / 2.4e9))
+    assert g1["mallStretch"] == pytest.approx(1.1 + 0.4 * (g1["mallLoad"] - 1.0) / 0.5)
+    assert g1["mallStretch"] == pytest.approx(1.31376, abs=1e-5)
+    assert g1["tStepCycles"] == pytest.approx(1024 * g1["mallStretch"])
+    g4 = RM.predict(hw, groupM=4, **cfg)
+    assert g4["refillMissShare"] == pytest.approx(0.1875)
+    assert g4["mallLoad"] == pytest.approx(0.4608, abs=1e-6) and g4["mallStretch"] == 1.0
+    assert g4["tStepCycles"] == pytest.approx(1024.0)
+    assert g1["predictedTFLOPS"] < g4["predictedTFLOPS"]
+    # Beyond the last point the path's bandwidth binds: stretch proportional to load.
+    steep = tmp_path / "steep.json"
+    steep.write_text(_CDNA4_JSON % curve.replace('"mallRefillBytesPerSec": 8e12', '"mallRefillBytesPerSec": 4e12'))
+    g1s = RM.predict(RM.Hardware(str(steep)), groupM=1, **cfg)
+    assert g1s["mallLoad"] == pytest.approx(2 * g1["mallLoad"])
+    assert g1s["mallStretch"] == pytest.approx(2.0 * g1s["mallLoad"] / 2.0)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % curve.replace('"mallStretchLoad2": 1.0', '"mallStretchLoad2": 0.4'))
+    with pytest.raises(ValueError, match="mallStreamModel 1"):
+        RM.Hardware(str(bad))
+
+
+def test_hbm_write_model_prices_c_at_the_write_rate(tmp_path):
+    """hbmWriteModel 1 with reads at 8 TB/s and writes at 4 TB/s, on one XCD so
+    that the 256 resident 128x128 tiles of 2048 x 2048 x 128 fetch every panel
+    once: reads (2048 x 128 x 2) x 2 = 1,048,576 B, C 2048^2 x 2 = 8,388,608 B,
+    2^30 FLOP: 1,048,576 / 8e12 + 8,388,608 / 4e12 = 2.228224 us, 481.882
+    TFLOP/s (one rate for all 9,437,184 B: 910.222)."""
+    base = ', "numXcds": 1'
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % base)
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % (base + ', "hbmWriteModel": 1, "hbmWriteBytesPerSec": 4e12'))
+    cfg = dict(M=2048, N=2048, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128)
+    flops = 2.0 * 2048 * 2048 * 128
+    p_off = RM.predict(RM.Hardware(str(off)), **cfg)
+    p_on = RM.predict(RM.Hardware(str(on)), **cfg)
+    assert p_off["hbmTFLOPS"] == pytest.approx(flops / (9437184 / 8e12) / 1e12)
+    assert p_on["hbmTFLOPS"] == pytest.approx(flops / (1048576 / 8e12 + 8388608 / 4e12) / 1e12)
+    assert p_on["hbmTFLOPS"] == pytest.approx(481.882, abs=1e-3)
+    assert p_on["arithmeticIntensity"] == pytest.approx(flops / 9437184)
+    # The drain of each tile moves at the write rate: twice the cycles.
+    assert p_on["tEpilogueCycles"] == pytest.approx(2 * p_off["tEpilogueCycles"])
+
+
+def test_fill_latency_model_adds_one_wait_per_round(tmp_path):
+    """fillLatencyModel 1 with fillLatencySec 1 us: the prediction's time grows by
+    one microsecond per round of one-tile-per-workgroup workgroups (fullWaves)
+    and by one for a persistent grid, whatever its tile count."""
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % "")
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % ', "fillLatencyModel": 1, "fillLatencySec": 1e-6')
+    hw_off, hw_on = RM.Hardware(str(off)), RM.Hardware(str(on))
+    for cfg, rounds in [
+        (dict(M=4096, N=4096, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128), None),
+        (dict(M=8192, N=8192, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=4, regsPerThread=185,
+              schedule=2), 1.0),
+    ]:
+        a, b = RM.predict(hw_off, **cfg), RM.predict(hw_on, **cfg)
+        want_rounds = rounds if rounds is not None else math.ceil(a["wavesExact"])
+        assert b["fillRounds"] == want_rounds
+        flops = 2.0 * cfg["M"] * cfg["N"] * cfg["K"]
+        assert b["predictedTFLOPS"] == pytest.approx(flops / (flops / (a["predictedTFLOPS"] * 1e12) +
+                                                             want_rounds * 1e-6) / 1e12)
+        assert b["predictedTFLOPS"] == pytest.approx(min(b["computeTFLOPS"], b["hbmTFLOPS"]))
