@@ -1,24 +1,29 @@
 """Cross-check of the cost model's bottleneck labels against rocprofv3 counters:
 the MI355X restatement of the reference's bench/run-ncu-validation.sh and its
-pre-registered decision table (data/sweep/ncu-label-mapping.md).
+pre-registered decision tables (data/sweep/ncu-label-mapping.md).
 
-    python -m ridge_amd.labelcheck select          # the registered config list
-    python -m ridge_amd.labelcheck run             # the launches, under rocprofv3
-    python -m ridge_amd.labelcheck gather --counters D1 --fetch D2 --write D3 --trace D4
-    python -m ridge_amd.labelcheck score           # the registered decision table
+    python -m ridge_amd.labelcheck [--registration N] select   # the registered config list
+    python -m ridge_amd.labelcheck [--registration N] run      # the launches, under rocprofv3
+    python -m ridge_amd.labelcheck [--registration N] gather --counters D1 --fetch D2 --write D3 --trace D4
+    python -m ridge_amd.labelcheck [--registration N] score    # the registered decision table
 
-The decision table, the counters, the config-selection rule and the pass
-criterion are fixed in data/sweep/rocprof-label-mapping.md and
-data/sweep/rocprof-label-configs.csv, both committed before the first run.
+Each registration fixes, in files committed before its first run, the decision
+table, the counters, the config-selection rule, the pass criterion and a frozen
+copy of the calibration and of the measured rows the selection was made from:
+  1  data/sweep/rocprof-label-mapping.md (scored 5 of 13: FAIL; stands as is)
+  2  data/sweep/rocprof-label2-mapping.md (the current kernel table and model;
+     ENVELOPE decided from durations at K and 16 K, HBM% against the calibrated
+     read and write rates, no fall-through label)
 `run` and `gather` only launch kernels and collect numbers; `score` applies the
 registered table and nothing else, so the rule cannot drift after the data
 exists (the reference's own discipline, run-ncu-validation.sh:1-6).
 
 `run` must be the program rocprofv3 starts (`rocprofv3 ... -- python3 -m
 ridge_amd.labelcheck run`). It launches, for every config in order, the
-registered variant LAUNCHES times on seeded U[-1,1) inputs; `gather` assigns the
-GEMM dispatches of each rocprofv3 pass to configs by dispatch order and checks
-every dispatch's kernel name against the config's template arguments.
+registered variant LAUNCHES times on seeded U[-1,1) inputs (and, for a
+registration with a long factor F, LAUNCHES more times at K x F); `gather`
+assigns the GEMM dispatches of each rocprofv3 pass to configs by dispatch order
+and checks every dispatch's kernel name against the config's template arguments.
 """
 
 import argparse
@@ -34,18 +39,34 @@ from ridge_amd import model as RM
 from ridge_amd import tables as T
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-# The calibration the registration was made under (a frozen copy of
-# data/hardware/mi355x.json at registration time): selection and scoring use it,
-# so a later re-calibration cannot change the registered configs or thresholds.
-HW_JSON = os.path.join(ROOT, "data", "sweep", "rocprof-label-hw.json")
-# The measured rows the selection was made from (frozen copies of
-# data/measured/mi355x.csv and mi355x-baseline-configs.csv at registration
-# time), for the same reason: re-measuring the sweep after a kernel change must
-# not change the registered configs.
-SOURCES = [os.path.join(ROOT, "data", "sweep", "rocprof-label-sweep.csv"),
-           os.path.join(ROOT, "data", "sweep", "rocprof-label-baseline-configs.csv")]
-CONFIGS_CSV = os.path.join(ROOT, "data", "sweep", "rocprof-label-configs.csv")
-COUNTERS_CSV = os.path.join(ROOT, "data", "measured", "rocprof-labels.csv")
+SWEEP_DIR = os.path.join(ROOT, "data", "sweep")
+
+
+class Registration:
+    """The files of one registration. `hw_json` is a frozen copy of
+    data/hardware/mi355x.json at registration time and `sources` frozen copies
+    of the measured rows the selection was made from, so a later re-calibration
+    or re-measurement cannot change the registered configs or thresholds.
+    `long_factor` F > 0 adds LAUNCHES launches of every config at K x F."""
+
+    def __init__(self, number, stem, long_factor):
+        self.number = number
+        self.mapping = os.path.join(SWEEP_DIR, stem + "-mapping.md")
+        self.hw_json = os.path.join(SWEEP_DIR, stem + "-hw.json")
+        self.sources = [os.path.join(SWEEP_DIR, stem + "-sweep.csv"),
+                        os.path.join(SWEEP_DIR, stem + "-baseline-configs.csv")]
+        self.configs = os.path.join(SWEEP_DIR, stem + "-configs.csv")
+        self.counters = os.path.join(ROOT, "data", "measured", stem.replace("rocprof-label", "rocprof-labels") + ".csv")
+        self.long_factor = long_factor
+
+
+REGISTRATIONS = {1: Registration(1, "rocprof-label", 0), 2: Registration(2, "rocprof-label2", 16)}
+CURRENT = 2
+# Registration 1's files under their original names (kept for its tests).
+HW_JSON = REGISTRATIONS[1].hw_json
+SOURCES = REGISTRATIONS[1].sources
+CONFIGS_CSV = REGISTRATIONS[1].configs
+COUNTERS_CSV = REGISTRATIONS[1].counters
 
 LAUNCHES = 3
 PER_LABEL = 4
@@ -77,39 +98,67 @@ def _read_rows(path):
     return T.read(path).records
 
 
-def predict_row(hw, r):
+def predict_row(hw, r, with_schedule=False):
+    """The model on a measured row. Registration 2 passes the row's schedule (the
+    persistent rows are modelled as such); registration 1 did not, and keeps
+    selecting as it did."""
+    extra = {"schedule": int(r["schedule"])} if with_schedule and "schedule" in r else {}
     return RM.predict(hw, M=int(r["M"]), N=int(r["N"]), K=int(r["K"]), BM=int(r["BM"]), BN=int(r["BN"]),
                       BK=int(r["BK"]), warpM=int(r["WM"]), warpN=int(r["WN"]), stages=int(r["stages"]),
-                      regsPerThread=int(r["regsPerThread"]), groupM=int(r["groupM"]))
+                      regsPerThread=int(r["regsPerThread"]), groupM=int(r["groupM"]), **extra)
 
 
-def _config_row(label, r, p):
-    return {"predicted_label": label, "model_label": p["bottleneck"], "tag": r["tag"], "M": int(r["M"]),
-            "N": int(r["N"]), "K": int(r["K"]), **{k: int(r[k]) for k in KEY_FIELDS},
-            "regsPerThread": int(r["regsPerThread"]), "theoretical_waves_per_cu": p["ctasPerSM"] * p["numWarps"],
-            "pred_tflops": round(p["predictedTFLOPS"], 3), "measured_tflops": float(r["tflops"])}
+def _config_row(label, r, p, why=None):
+    row = {"predicted_label": label, "model_label": p["bottleneck"], "tag": r["tag"], "M": int(r["M"]),
+           "N": int(r["N"]), "K": int(r["K"]), **{k: int(r[k]) for k in KEY_FIELDS},
+           "regsPerThread": int(r["regsPerThread"]), "theoretical_waves_per_cu": p["ctasPerSM"] * p["numWarps"],
+           "pred_tflops": round(p["predictedTFLOPS"], 3), "measured_tflops": float(r["tflops"])}
+    if why is not None:
+        row["schedule"] = int(r["schedule"])
+        row["why"] = why
+    return row
 
 
-def select_configs(sources=SOURCES, hw_json=HW_JSON, per_label=PER_LABEL):
+def _key(r):
+    return tuple(int(r[k]) for k in ["M", "N", "K"] + KEY_FIELDS)
+
+
+# Registration 2's required configs, scored beside the per-label selection:
+# (shape + tile key, reason). The headline row also serves as the control.
+REQUIRED_2 = [
+    ((4096, 4096, 4096, 256, 256, 32, 128, 64, 3, 4), "headline ping-pong row"),
+    ((4096, 4096, 4096, 256, 128, 64, 64, 64, 3, 8), "8-wave ping-pong row, 256x128 tile"),
+    ((8192, 8192, 128, 128, 128, 64, 64, 64, 4, 8), "persistent row, K = 128"),
+    ((8192, 8192, 128, 256, 128, 32, 64, 64, 6, 4), "persistent row, K = 128"),
+    ((16384, 128, 8192, 128, 64, 64, 64, 32, 6, 8), "persistent row, tall-skinny"),
+]
+CONTROL_2 = REQUIRED_2[0][0]
+
+
+def select_configs(sources=SOURCES, hw_json=HW_JSON, per_label=PER_LABEL, registration=1):
     """The registered selection rule: every measured row (sweep and BASELINE
     configs) is labelled by the model; within each label the rows are sorted by
     (tag, BM, BN, BK, WM, WN, stages, groupM) and the first `per_label` rows of
     distinct shapes are taken (the reference's rule, ncu-label-mapping.md
-    section 3)."""
+    section 3). Registration 2 labels with each row's schedule and adds the
+    configs of REQUIRED_2 that the rule did not pick."""
+    second = registration == 2
     hw = RM.Hardware(hw_json)
-    groups = {}
+    groups, by_key = {}, {}
     for src in sources:
         for r in _read_rows(src):
-            p = predict_row(hw, r)
+            p = predict_row(hw, r, second)
             groups.setdefault(p["bottleneck"], []).append((r, p))
+            by_key.setdefault(_key(r), (r, p))
     out = []
-    # The headline bench config, a registered control outside the score: its
-    # one-workgroup-per-CU grid keeps every CU busy for the whole launch, which
-    # checks the counter normalisations (section 2 of the registration).
+    # The control: one workgroup per CU for the whole launch keeps every CU busy,
+    # which checks the counter normalisations (section 2 of each registration).
+    control = CONTROL_2 if second else CONTROL
     for r in _read_rows(sources[-1]):
-        if tuple(int(r[k]) for k in ["M", "N", "K"] + KEY_FIELDS) == CONTROL:
-            p = predict_row(hw, r)
-            out.append(_config_row("CONTROL", r, p))
+        if _key(r) == control:
+            p = predict_row(hw, r, second)
+            out.append(_config_row("CONTROL", r, p, "control" if second else None))
+    picked = set()
     for label in LABEL_ORDER:
         rows = sorted(groups.get(label, []),
                       key=lambda rp: (rp[0]["tag"],) + tuple(int(rp[0][k]) for k in KEY_FIELDS))
@@ -119,28 +168,34 @@ def select_configs(sources=SOURCES, hw_json=HW_JSON, per_label=PER_LABEL):
             if shape in shapes:
                 continue
             shapes.add(shape)
-            out.append(_config_row(label, r, p))
+            picked.add(_key(r))
+            out.append(_config_row(label, r, p, "per-label rule" if second else None))
             if len(shapes) == per_label:
                 break
+    if second:
+        for key, why in REQUIRED_2:
+            if key in picked:
+                continue
+            r, p = by_key[key]
+            out.append(_config_row(p["bottleneck"], r, p, "required: " + why))
     return out
 
 
 CONFIG_COLUMNS = ["predicted_label", "model_label", "tag", "M", "N", "K"] + KEY_FIELDS + \
     ["regsPerThread", "theoretical_waves_per_cu", "pred_tflops", "measured_tflops"]
+CONFIG_COLUMNS_2 = CONFIG_COLUMNS + ["schedule", "why"]
 
 
 def cmd_select(args):
-    rows = select_configs()
-    with open(args.out, "w", newline="") as f:
-        f.write("# registered before any rocprofv3 run; see data/sweep/rocprof-label-mapping.md\n")
-        w = csv.DictWriter(f, fieldnames=CONFIG_COLUMNS)
-        w.writeheader()
-        for r in rows:
-            w.writerow(r)
+    reg = REGISTRATIONS[args.registration]
+    rows = select_configs(reg.sources, reg.hw_json, registration=reg.number)
+    cols = CONFIG_COLUMNS_2 if reg.number == 2 else CONFIG_COLUMNS
+    out = args.out or reg.configs
+    T.write(out, cols, rows, ["registered before any rocprofv3 run; see %s" % os.path.relpath(reg.mapping, ROOT)])
     for r in rows:
-        print("%-9s %-28s %6dx%-6dx%-5d %dx%dx%d w%dx%d s%d g%d" % (
-            r["predicted_label"], r["tag"], r["M"], r["N"], r["K"], *[r[k] for k in KEY_FIELDS]))
-    print("wrote %d configs to %s" % (len(rows), args.out))
+        print("%-9s %-28s %6dx%-6dx%-5d %dx%dx%d w%dx%d s%d g%d %s" % (
+            r["predicted_label"], r["tag"], r["M"], r["N"], r["K"], *[r[k] for k in KEY_FIELDS], r.get("why", "")))
+    print("wrote %d configs to %s" % (len(rows), out))
 
 
 def load_configs(path=CONFIGS_CSV):
@@ -153,40 +208,41 @@ def load_configs(path=CONFIGS_CSV):
 
 def cmd_run(args):
     """The launches rocprofv3 observes: per config, LAUNCHES launches of the
-    registered variant, each followed by a synchronize."""
+    registered variant, each followed by a synchronize; with a long factor F,
+    LAUNCHES more at K x F (the steady-state reference of the ENVELOPE rule)."""
     import torch
     from ridge_amd import gemm as G
-    configs = load_configs(args.configs)
+    reg = REGISTRATIONS[args.registration]
+    configs = load_configs(args.configs or reg.configs)
     dev = "cuda:0"
-    cache = {}
     for i, c in enumerate(configs):
         idx = G.find_variant(*[c[k] for k in KEY_FIELDS])
         if idx < 0:
             raise SystemExit("config %d: variant not in the kernel table (a row retired after the "
                              "registration; its counters were gathered and scored before, and a replay "
                              "needs the table of the registration commit)" % i)
-        if not G.variant(idx).divides(c["M"], c["N"], c["K"]):
-            raise SystemExit("config %d: variant does not divide the shape" % i)
-        M, N, K = c["M"], c["N"], c["K"]
-        print("config %d/%d %s %dx%dx%d %s" % (i + 1, len(configs), c["predicted_label"], M, N, K,
-                                               G.variant(idx).label()), flush=True)
-        if (M, N, K) not in cache:
-            cache.clear()
+        for factor in ([1, reg.long_factor] if reg.long_factor else [1]):
+            M, N, K = c["M"], c["N"], c["K"] * factor
+            if not G.variant(idx).divides(M, N, K):
+                raise SystemExit("config %d: variant does not divide %dx%dx%d" % (i, M, N, K))
+            print("config %d/%d %s %dx%dx%d %s" % (i + 1, len(configs), c["predicted_label"], M, N, K,
+                                                   G.variant(idx).label()), flush=True)
             torch.cuda.synchronize()
             A = torch.empty((M, K), dtype=torch.float16, device=dev)
             B = torch.empty((K, N), dtype=torch.float16, device=dev)
             C = torch.empty((M, N), dtype=torch.float16, device=dev)
             G.fill_uniform(A, 1)
             G.fill_uniform(B, 2)
-            cache[(M, N, K)] = (A, B, C)
-        A, B, C = cache[(M, N, K)]
-        torch.cuda.synchronize()
-        for _ in range(args.launches):
-            rc = G.launch(idx, A, B, C, M, N, K)
-            if rc != 0:
-                raise SystemExit("config %d: launch returned %d" % (i, rc))
             torch.cuda.synchronize()
-    print("labelcheck run: %d configs x %d launches" % (len(configs), args.launches), flush=True)
+            for _ in range(args.launches):
+                rc = G.launch(idx, A, B, C, M, N, K)
+                if rc != 0:
+                    raise SystemExit("config %d: launch returned %d" % (i, rc))
+                torch.cuda.synchronize()
+            del A, B, C
+    print("labelcheck run: %d configs x %d launches%s" % (
+        len(configs), args.launches, " (and as many at K x %d)" % reg.long_factor if reg.long_factor else ""),
+        flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -195,7 +251,7 @@ def cmd_run(args):
 
 # Kernel names as rocprofv3 reports them: Itanium-mangled, each int template
 # argument as Li<n>E (gemmMfmaKernelILi64ELi64E...), or demangled (<64, 64, ...>).
-_GEMM_NAME = re.compile(r"gemmMfma(?:PingPong)?Kernel(?:I" + r"Li(\d+)E" * 7 + r"|<" +
+_GEMM_NAME = re.compile(r"gemmMfma(?:PingPong|Persistent)?Kernel(?:I" + r"Li(\d+)E" * 7 + r"|<" +
                         r",".join([r"\s*(\d+)"] * 7) + r"\s*>)")
 
 
@@ -235,8 +291,9 @@ def parse_trace_dir(directory):
 
 
 def gemm_dispatches(parsed, configs, launches):
-    """The GEMM dispatches in dispatch order, grouped per config; each name must
-    carry that config's template arguments."""
+    """The GEMM dispatches in dispatch order, grouped per config (`launches` per
+    config, twice that for a registration with a long factor: the K launches
+    first); each name must carry that config's template arguments."""
     gemm = [(k, v) for k, v in sorted(parsed.items()) if _GEMM_NAME.search(v["name"])]
     if len(gemm) != len(configs) * launches:
         raise SystemExit("expected %d GEMM dispatches, found %d" % (len(configs) * launches, len(gemm)))
@@ -264,33 +321,34 @@ def _counter(dispatch, name, xcds, grbm):
 
 
 def cmd_gather(args):
-    configs = load_configs(args.configs)
-    with open(HW_JSON) as f:
+    reg = REGISTRATIONS[args.registration]
+    configs = load_configs(args.configs or reg.configs)
+    with open(reg.hw_json) as f:
         hwj = json.load(f)
     xcds = int(hwj.get("numXcds", 8))
-    p1 = gemm_dispatches(parse_counter_dir(args.counters), configs, args.launches)
-    pf = gemm_dispatches(parse_counter_dir(args.fetch), configs, args.launches)
-    pw = gemm_dispatches(parse_counter_dir(args.write), configs, args.launches)
-    pt = gemm_dispatches(parse_trace_dir(args.trace), configs, args.launches)
+    per = args.launches * (2 if reg.long_factor else 1)
+    p1 = gemm_dispatches(parse_counter_dir(args.counters), configs, per)
+    pf = gemm_dispatches(parse_counter_dir(args.fetch), configs, per)
+    pw = gemm_dispatches(parse_counter_dir(args.write), configs, per)
+    pt = gemm_dispatches(parse_trace_dir(args.trace), configs, per)
+    n = args.launches
     rows = []
+    cols = CONFIG_COLUMNS_2 if reg.number == 2 else CONFIG_COLUMNS
     for i, c in enumerate(configs):
         med = lambda xs: statistics.median(xs)  # noqa: E731
-        row = {k: c[k] for k in CONFIG_COLUMNS}
+        row = {k: c[k] for k in cols}
         for name in PASS1_COUNTERS:
-            row[name] = med([_counter(d, name, xcds, name.startswith("GRBM_")) for d in p1[i]])
-        row["FETCH_SIZE"] = med([_counter(d, "FETCH_SIZE", xcds, False) for d in pf[i]])
-        row["WRITE_SIZE"] = med([_counter(d, "WRITE_SIZE", xcds, False) for d in pw[i]])
-        row["duration_ns"] = med([d["ns"] for d in pt[i]])
+            row[name] = med([_counter(d, name, xcds, name.startswith("GRBM_")) for d in p1[i][:n]])
+        row["FETCH_SIZE"] = med([_counter(d, "FETCH_SIZE", xcds, False) for d in pf[i][:n]])
+        row["WRITE_SIZE"] = med([_counter(d, "WRITE_SIZE", xcds, False) for d in pw[i][:n]])
+        row["duration_ns"] = med([d["ns"] for d in pt[i][:n]])
+        if reg.long_factor:
+            row["long_duration_ns"] = med([d["ns"] for d in pt[i][n:]])
         rows.append(row)
-    cols = list(rows[0].keys())
-    with open(args.out, "w", newline="") as f:
-        f.write("# rocprofv3 counters per registered config (medians over %d launches); GRBM counters per XCD\n"
-                % args.launches)
-        w = csv.DictWriter(f, fieldnames=cols)
-        w.writeheader()
-        for r in rows:
-            w.writerow(r)
-    print("wrote %d rows to %s" % (len(rows), args.out))
+    out = args.out or reg.counters
+    T.write(out, list(rows[0].keys()), rows,
+            ["rocprofv3 counters per registered config (medians over %d launches); GRBM counters per XCD" % n])
+    print("wrote %d rows to %s" % (len(rows), out))
 
 
 # ---------------------------------------------------------------------------
@@ -332,16 +390,56 @@ def counter_label(d):
     return "ENVELOPE"
 
 
-def score(rows, hwj):
+# Registration 2's decision table (data/sweep/rocprof-label2-mapping.md section 2).
+STEADY_SHARE_MIN = 0.80     # rule 2: steady-state share below 0.80 -> ENVELOPE (or WAVES, the worse)
+
+
+def derived2(row, hwj, long_factor):
+    """Registration 2's quantities: registration 1's, with HBM% as the share of
+    the launch the DRAM traffic needs at the calibrated read and write rates, and
+    the steady-state share s = t(K x F) / (F t(K)), the launch's time at K against
+    F times its time per K at K x F (where fill and drain are amortised)."""
+    d = derived(row, hwj)
+    read = float(row["FETCH_SIZE"]) * FETCH_SCALE * 1024.0
+    write = float(row["WRITE_SIZE"]) * WRITE_SCALE * 1024.0
+    dur = float(row["duration_ns"]) * 1e-9
+    d["hbm_pct"] = 100.0 * (read / float(hwj["hbmBytesPerSec"]) + write / float(hwj["hbmWriteBytesPerSec"])) / dur
+    d["steady_share"] = float(row["long_duration_ns"]) / (long_factor * float(row["duration_ns"]))
+    return d
+
+
+def counter_label2(d):
+    """Registration 2's table, first match wins; a row no rule claims is
+    UNDECIDED (scored as a disagreement: there is no fall-through label)."""
+    if d["hbm_pct"] >= HBM_PCT_MIN:
+        return "HBM"
+    busy = d["simd_util_pct"] / 100.0
+    if d["steady_share"] < STEADY_SHARE_MIN or busy < SIMD_UTIL_PCT_MAX / 100.0:
+        return "ENVELOPE" if d["steady_share"] < busy else "WAVES"
+    if d["occ_pct"] / d["theoretical_occ_pct"] < OCC_SHORTFALL_MAX:
+        return "OCC"
+    if d["lds_pct"] > d["mfma_pct"]:
+        return "SMEM"
+    if d["mfma_pct"] >= MFMA_PCT_MIN:
+        return "TENSOR_CORE"
+    return "UNDECIDED"
+
+
+def score(rows, hwj, registration=1):
     """(results, agree, need, control_ok): results over every row, the count of
     scored rows (the control excluded) whose counter label equals the model's,
     the registered pass threshold, and whether the control's SIMD utilisation
     is in its band (if not, the normalisations are wrong and the run is void)."""
     results = []
     control_ok = True
+    reg = REGISTRATIONS[registration]
     for r in rows:
-        d = derived(r, hwj)
-        results.append((r, d, counter_label(d)))
+        if registration == 2:
+            d = derived2(r, hwj, reg.long_factor)
+            results.append((r, d, counter_label2(d)))
+        else:
+            d = derived(r, hwj)
+            results.append((r, d, counter_label(d)))
         if r["predicted_label"] == "CONTROL":
             lo, hi = CONTROL_SIMD_UTIL_PCT
             control_ok = control_ok and lo <= d["simd_util_pct"] <= hi
@@ -352,21 +450,23 @@ def score(rows, hwj):
 
 
 def cmd_score(args):
-    with open(HW_JSON) as f:
+    reg = REGISTRATIONS[args.registration]
+    with open(reg.hw_json) as f:
         hwj = json.load(f)
-    rows = _read_rows(args.counters_csv)
-    results, agree, need, control_ok = score(rows, hwj)
-    print("%-9s %-28s %-22s %6s %6s %6s %6s %6s %6s  %-9s" % (
-        "model", "shape", "variant", "HBM%", "SIMD%", "occ%", "theo%", "LDS%", "MFMA%", "counters"))
+    rows = _read_rows(args.counters_csv or reg.counters)
+    results, agree, need, control_ok = score(rows, hwj, reg.number)
+    print("%-9s %-28s %-22s %6s %6s %6s %6s %6s %6s %6s  %-9s" % (
+        "model", "shape", "variant", "HBM%", "SIMD%", "occ%", "theo%", "LDS%", "MFMA%", "steady", "counters"))
     by_label = {}
     for r, d, lab in results:
         shape = "%sx%sx%s" % (r["M"], r["N"], r["K"])
         var = "%sx%sx%s w%sx%s s%s g%s" % tuple(r[k] for k in KEY_FIELDS)
         verdict = "" if r["predicted_label"] == "CONTROL" else (
             "agree" if lab == r["predicted_label"] else "DISAGREE")
-        print("%-9s %-28s %-22s %6.1f %6.1f %6.1f %6.1f %6.1f %6.1f  %-9s %s" % (
+        print("%-9s %-28s %-22s %6.1f %6.1f %6.1f %6.1f %6.1f %6.1f %6s  %-9s %s" % (
             r["predicted_label"], shape, var, d["hbm_pct"], d["simd_util_pct"], d["occ_pct"],
-            d["theoretical_occ_pct"], d["lds_pct"], d["mfma_pct"], lab, verdict))
+            d["theoretical_occ_pct"], d["lds_pct"], d["mfma_pct"],
+            "%.3f" % d["steady_share"] if "steady_share" in d else "-", lab, verdict))
         if r["predicted_label"] == "CONTROL":
             continue
         s = by_label.setdefault(r["predicted_label"], [0, 0])
@@ -376,8 +476,8 @@ def cmd_score(args):
     for lab in LABEL_ORDER:
         if lab in by_label:
             print("  %-9s %d of %d agree%s" % (lab, by_label[lab][0], by_label[lab][1],
-                                              "  (fall-through label: weakest evidence)" if lab == "ENVELOPE"
-                                              else ""))
+                                              "  (fall-through label: weakest evidence)"
+                                              if lab == "ENVELOPE" and reg.number == 1 else ""))
     if not control_ok:
         print("\ncontrol SIMD utilisation outside [%g, %g]%%: the normalisations are wrong, the run is VOID"
               % CONTROL_SIMD_UTIL_PCT)
@@ -390,20 +490,21 @@ def cmd_score(args):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
+    ap.add_argument("--registration", type=int, default=CURRENT, choices=sorted(REGISTRATIONS))
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("select")
-    s.add_argument("--out", default=CONFIGS_CSV)
+    s.add_argument("--out", default=None)
     r = sub.add_parser("run")
-    r.add_argument("--configs", default=CONFIGS_CSV)
+    r.add_argument("--configs", default=None)
     r.add_argument("--launches", type=int, default=LAUNCHES)
     g = sub.add_parser("gather")
-    g.add_argument("--configs", default=CONFIGS_CSV)
+    g.add_argument("--configs", default=None)
     g.add_argument("--launches", type=int, default=LAUNCHES)
     for k in ("counters", "fetch", "write", "trace"):
         g.add_argument("--" + k, required=True)
-    g.add_argument("--out", default=COUNTERS_CSV)
+    g.add_argument("--out", default=None)
     c = sub.add_parser("score")
-    c.add_argument("--counters-csv", default=COUNTERS_CSV)
+    c.add_argument("--counters-csv", default=None)
     args = ap.parse_args(argv)
     return {"select": cmd_select, "run": cmd_run, "gather": cmd_gather, "score": cmd_score}[args.cmd](args)
 

@@ -28,14 +28,17 @@ def splitmix64_at(seed, i):
     return z ^ (z >> 31)
 
 
-def registered_shapes(seed=DEFAULT_SEED, count=14):
+def registered_shapes(seed=DEFAULT_SEED, count=14, exclude=()):
+    """`count` distinct shapes drawn in order; a draw already taken, or listed in
+    `exclude` (the shapes of another registered sweep, for a held-out set),
+    is redrawn."""
     shapes, i = [], 0
     while len(shapes) < count:
         M = MN_CHOICES[splitmix64_at(seed, i) % len(MN_CHOICES)]
         N = MN_CHOICES[splitmix64_at(seed, i + 1) % len(MN_CHOICES)]
         K = K_CHOICES[splitmix64_at(seed, i + 2) % len(K_CHOICES)]
         i += 3
-        if (M, N, K) not in shapes:
+        if (M, N, K) not in shapes and (M, N, K) not in exclude:
             shapes.append((M, N, K))
     return shapes
 
@@ -56,15 +59,14 @@ BASELINE_SHAPES = [
 ]
 
 
-def write_registered(path, seed=DEFAULT_SEED):
+def write_registered(path, seed=DEFAULT_SEED, prefix="s", exclude=(), note=()):
     lines = [
         "# MI355X registered sweep: 14 shapes drawn by ridge_amd/sweep.py with seed 0x%X." % seed,
         "# Registered before any measurement. The tile configs are the kernel table",
         "# (ridge_amd/csrc/gemm_variants.def); the sweep is every shape x every variant.",
-        "# M,N,K,tag,rationale",
-    ]
-    for i, (M, N, K) in enumerate(registered_shapes(seed)):
-        lines.append("%d,%d,%d,s%02d-%dx%dx%d,%s" % (M, N, K, i, M, N, K, rationale(M, N, K)))
+    ] + ["# " + n for n in note] + ["# M,N,K,tag,rationale"]
+    for i, (M, N, K) in enumerate(registered_shapes(seed, exclude=exclude)):
+        lines.append("%d,%d,%d,%s%02d-%dx%dx%d,%s" % (M, N, K, prefix, i, M, N, K, rationale(M, N, K)))
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")
 
@@ -83,11 +85,20 @@ def main(argv=None):
     ap.add_argument("--seed", type=lambda s: int(s, 0), default=DEFAULT_SEED)
     ap.add_argument("--out", default="data/sweep/mi355x-registered.csv")
     ap.add_argument("--baseline-out", default="data/sweep/mi355x-baseline-configs.csv")
+    ap.add_argument("--tag-prefix", default="s", help="first letter(s) of every shape tag")
+    ap.add_argument("--exclude", default=None,
+                    help="a registered sweep whose shapes this one must not repeat (a held-out set)")
+    ap.add_argument("--note", action="append", default=[], help="an extra header line")
     args = ap.parse_args(argv)
     os.makedirs(os.path.dirname(args.out) or ".", exist_ok=True)
-    write_registered(args.out, args.seed)
-    write_baseline(args.baseline_out)
-    print("wrote", args.out, "and", args.baseline_out)
+    exclude = ()
+    if args.exclude:
+        from ridge_amd import tables as T
+        exclude = [s[:3] for s in T.read_shapes(args.exclude)]
+    write_registered(args.out, args.seed, args.tag_prefix, exclude, args.note)
+    if args.baseline_out != "-":
+        write_baseline(args.baseline_out)
+    print("wrote", args.out, "" if args.baseline_out == "-" else "and " + args.baseline_out)
 
 
 if __name__ == "__main__":

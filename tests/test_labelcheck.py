@@ -16,7 +16,7 @@ def test_committed_config_list_is_the_registered_selection(tmp_path):
     """Re-running the registered selection gives the committed configs and labels
     (measured_tflops is informational: the value the sweep held at registration)."""
     out = tmp_path / "c.csv"
-    LC.main(["select", "--out", str(out)])
+    LC.main(["--registration", "1", "select", "--out", str(out)])
     keep = [c for c in LC.CONFIG_COLUMNS if c != "measured_tflops"]
     now = [{k: r[k] for k in keep} for r in LC._read_rows(str(out))]
     committed = [{k: r[k] for k in keep} for r in LC._read_rows(LC.CONFIGS_CSV)]
@@ -139,3 +139,67 @@ def test_committed_counters_score_as_reported():
             s[0] += lab == r["predicted_label"]
             s[1] += 1
     assert split == {"SMEM": [0, 4], "WAVES": [4, 4], "ENVELOPE": [0, 4], "HBM": [1, 1]}
+
+
+REG2 = LC.REGISTRATIONS[2]
+
+
+def test_registration_2_committed_configs_are_its_selection(tmp_path):
+    """Registration 2's committed config list re-derives from its frozen files,
+    holds every required config, and is the control plus 21 scored configs."""
+    out = tmp_path / "c2.csv"
+    LC.main(["--registration", "2", "select", "--out", str(out)])
+    keep = [c for c in LC.CONFIG_COLUMNS_2 if c != "measured_tflops"]
+    now = [{k: r[k] for k in keep} for r in LC._read_rows(str(out))]
+    committed = [{k: r[k] for k in keep} for r in LC._read_rows(REG2.configs)]
+    assert now == committed
+    rows = LC.load_configs(REG2.configs)
+    assert rows[0]["predicted_label"] == "CONTROL" and len(rows) == 22
+    keys = {tuple(r[k] for k in ["M", "N", "K"] + LC.KEY_FIELDS) for r in rows[1:]}
+    for key, _why in LC.REQUIRED_2:
+        assert key in keys
+    assert all(r["model_label"] == r["predicted_label"] for r in rows[1:])
+
+
+def _d2(**kw):
+    base = dict(hbm_pct=10.0, simd_util_pct=99.0, occ_pct=25.0, theoretical_occ_pct=25.0, lds_pct=20.0,
+                mfma_pct=50.0, steady_share=0.95)
+    base.update(kw)
+    return base
+
+
+def test_registration_2_decision_table():
+    assert LC.counter_label2(_d2()) == "UNDECIDED"                          # no fall-through label
+    assert LC.counter_label2(_d2(hbm_pct=70.0, steady_share=0.1)) == "HBM"
+    assert LC.counter_label2(_d2(steady_share=0.79)) == "ENVELOPE"
+    assert LC.counter_label2(_d2(steady_share=0.80)) == "UNDECIDED"
+    assert LC.counter_label2(_d2(simd_util_pct=79.0)) == "WAVES"            # s 0.95 > 0.79
+    assert LC.counter_label2(_d2(simd_util_pct=60.0, steady_share=0.5)) == "ENVELOPE"   # the worse of the two
+    assert LC.counter_label2(_d2(simd_util_pct=40.0, steady_share=0.5)) == "WAVES"
+    assert LC.counter_label2(_d2(occ_pct=17.4)) == "OCC"
+    assert LC.counter_label2(_d2(lds_pct=50.1, mfma_pct=50.0)) == "SMEM"
+    assert LC.counter_label2(_d2(mfma_pct=70.0)) == "TENSOR_CORE"
+
+
+def test_registration_2_derived_quantities():
+    """HBM% at the two calibrated rates and the steady-state share."""
+    hwj = {"numSMs": 256, "simdsPerSM": 4, "maxWarpsPerSM": 32, "hbmBytesPerSec": 8e12,
+           "hbmWriteBytesPerSec": 4e12}
+    row = {"GRBM_GUI_ACTIVE": 1000.0, "GRBM_COUNT": 1000.0, "SQ_VALU_MFMA_BUSY_CYCLES": 512000.0,
+           "SQ_LDS_IDX_ACTIVE": 64000.0, "SQ_WAVE_CYCLES": 512000.0, "SQ_BUSY_CU_CYCLES": 256000.0,
+           "FETCH_SIZE": 1000.0, "WRITE_SIZE": 500.0, "duration_ns": 1000.0, "long_duration_ns": 12800.0,
+           "theoretical_waves_per_cu": 8}
+    d = LC.derived2(row, hwj, 16)
+    # reads 2000 KiB at 8 TB/s + writes 500 KiB at 4 TB/s, over 1 us
+    assert d["hbm_pct"] == pytest.approx(100.0 * (2048000 / 8e12 + 512000 / 4e12) / 1e-6)
+    assert d["steady_share"] == pytest.approx(12800.0 / (16 * 1000.0))
+
+
+def test_registration_2_text_matches_the_code():
+    text = open(REG2.mapping).read()
+    assert "| 1 | HBM%% ≥ %g | `HBM` |" % LC.HBM_PCT_MIN in text
+    assert "| 2 | s < %.2f or SIMD%% < %g |" % (LC.STEADY_SHARE_MIN, LC.SIMD_UTIL_PCT_MAX) in text
+    assert "| 6 | otherwise | `UNDECIDED` (a disagreement) |" in text
+    n = len(LC.load_configs(REG2.configs)) - 1
+    assert "%d scored configs (%d of %d)" % (n, -(-75 * n // 100), n) in text
+    assert "K × %d" % REG2.long_factor in text
