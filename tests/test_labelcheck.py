@@ -203,3 +203,21 @@ def test_registration_2_text_matches_the_code():
     n = len(LC.load_configs(REG2.configs)) - 1
     assert "%d scored configs (%d of %d)" % (n, -(-75 * n // 100), n) in text
     assert "K × %d" % REG2.long_factor in text
+
+
+def test_registration_2_counters_score_as_reported():
+    """Registration 2's committed counters through its registered table: 8 of 21
+    agree, FAIL (16 needed); the control is in band."""
+    import json
+    with open(REG2.hw_json) as f:
+        hwj = json.load(f)
+    rows = LC._read_rows(REG2.counters)
+    results, agree, need, control_ok = LC.score(rows, hwj, 2)
+    assert control_ok and (agree, need) == (8, 16)
+    split = {}
+    for r, d, lab in results:
+        if r["predicted_label"] != "CONTROL":
+            s = split.setdefault(r["predicted_label"], [0, 0])
+            s[0] += lab == r["predicted_label"]
+            s[1] += 1
+    assert split == {"SMEM": [0, 4], "WAVES": [3, 4], "ENVELOPE": [2, 5], "HBM": [3, 8]}
