@@ -7,6 +7,7 @@
                     [--allow-partitioned]
     python bench.py --mode copy     # plain device copy of known size, for scaling
                                     # rocprofv3 FETCH_SIZE / WRITE_SIZE counters
+    python bench.py --mode cold-split --steps 200   # which operand's cold lines cost a launch
 
 A step is one C = A * B launch (FP16 A, B row-major from a seeded U[-1,1) device
 fill, FP32 accumulate, FP16 C) through the C ABI, with inputs resident in HBM
@@ -38,7 +39,10 @@ model: the calibrated cost model's prediction for the measured variant and shape
 autotune: the metric's second half, the mean top-10 regret of the model-pruned
 autotuner, is computed from the committed measured sweep (data/measured/mi355x.csv,
 14 shapes x 24 variants) and the committed calibration (data/hardware/mi355x.json)
-by ridge_amd.autotune; it is a property of the sweep, not of this run's timing.
+by ridge_amd.autotune, with regret at top-1 and the expected regret of a random
+shortlist beside it, and the same for the held-out sweep registered before it was
+measured (data/measured/mi355x-heldout.csv, frozen constants); it is a property of
+the sweeps and the model, not of this run's timing.
 """
 
 import argparse
@@ -60,6 +64,8 @@ DEFAULT_VARIANT = (256, 256, 32, 128, 64, 3, 4)
 PROFILES = os.path.join(ROOT, "profiles")
 MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x.csv")
 HARDWARE_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+HELDOUT_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout.csv")
+HELDOUT_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout-hw.json")
 # Host threads for the CPU baseline: the cores this process may use, capped at
 # the 16 a GPU box grants one GPU.
 MAX_CPU_THREADS = 16
@@ -237,17 +243,36 @@ def measured_traffic(M, N, K, key):
 
 
 def autotune_regret(k=10):
-    """Mean and max regret at top-k over the committed sweep, or None if the model
-    CLI is not built."""
+    """The pruner's regret at top-1 and top-k with the random-shortlist baseline,
+    on the committed in-sample sweep (data/measured/mi355x.csv, 14 shapes x 24
+    variants, current calibration) and on the held-out sweep registered before it
+    was measured (data/measured/mi355x-heldout.csv, frozen constants); a property
+    of the sweeps and the model, not of this run's timing. None of it is
+    computed if the model CLI is not built."""
     try:
         from ridge_amd import autotune as AT
-        table, total, shapes, _ = AT.evaluate(MEASURED_SWEEP, HARDWARE_JSON, ks=(k,))
+        out = {"top_k": k, "source": "data/measured/mi355x.csv"}
+        for name, measured, hw in (("in_sample", MEASURED_SWEEP, HARDWARE_JSON),
+                                   ("held_out", HELDOUT_SWEEP, HELDOUT_HARDWARE_JSON)):
+            table, total, shapes, _ = AT.evaluate(measured, hw, ks=(1, k))
+            base = AT.baselines(measured, hw, ks=(1, k))
+            by_k = {r["k"]: r for r in table}
+            entry = {"mean_regret_pct": round(by_k[k]["mean_regret"], 3),
+                     "max_regret_pct": round(by_k[k]["max_regret"], 3), "exact_hits": by_k[k]["hits"],
+                     "regret_at_1_mean_pct": round(by_k[1]["mean_regret"], 3),
+                     "regret_at_1_max_pct": round(by_k[1]["max_regret"], 3),
+                     "random_pick_at_1_pct": round(base[1]["random"][0], 3),
+                     "random_pick_at_k_pct": round(base[k]["random"][0], 3),
+                     "shapes": shapes, "configs": total,
+                     "benchmarks_vs_exhaustive": round(by_k[k]["reduction"], 2),
+                     "source": os.path.relpath(measured, ROOT)}
+            if name == "in_sample":
+                out.update({key: v for key, v in entry.items() if key != "source"})
+            else:
+                out["held_out"] = entry
+        return out
     except Exception as e:  # the model CLI is part of the build; report its absence
         return {"error": "%s" % e}
-    row = table[0]
-    return {"top_k": k, "mean_regret_pct": round(row["mean_regret"], 3), "max_regret_pct": round(row["max_regret"], 3),
-            "exact_hits": row["hits"], "shapes": shapes, "configs": total,
-            "benchmarks_vs_exhaustive": round(row["reduction"], 2), "source": "data/measured/mi355x.csv"}
 
 
 def model_prediction(v, M, N, K, measured):
@@ -323,6 +348,53 @@ def run_copy_mode(steps):
     print(json.dumps({"mode": "copy", "bytes_per_copy": nbytes, "copies": steps}))
 
 
+def run_cold_split(args):
+    """Which operand's cold lines cost a launch: the GEMM (and hipBLASLt) timed
+    over 7 operand sets with only C rotated, only A and B rotated, or all three,
+    against one re-used set. Each figure is the middle of --repeats windows of
+    --steps launches after 1.5 s of the same rotation. Prints one JSON line (a
+    diagnostic, not the metric)."""
+    import torch
+    from ridge_amd import gemm as G
+    M, N, K = parse_ints(args.shape, 3)
+    idx = G.find_variant(*parse_ints(args.variant, 7))
+    if idx < 0 or not G.variant(idx).divides(M, N, K):
+        raise SystemExit("variant %s is not in the table or does not divide the shape" % args.variant)
+    stream = torch.cuda.current_stream()
+    n = 7
+    A = [torch.empty((M, K), dtype=torch.float16, device="cuda:0") for _ in range(n)]
+    B = [torch.empty((K, N), dtype=torch.float16, device="cuda:0") for _ in range(n)]
+    C = [torch.empty((M, N), dtype=torch.float16, device="cuda:0") for _ in range(n)]
+    for i in range(n):
+        G.fill_uniform(A[i], 1 + 2 * i)
+        G.fill_uniform(B[i], 2 + 2 * i)
+    torch.cuda.synchronize()
+    blas = G.BlasLt()
+    blas.prepare(A[0], B[0], C[0], M, N, K, candidates=16, iters=20, stream=stream)
+    kernels = {"ridge": lambda a, b, c: G.launch(idx, a, b, c, M, N, K, stream),
+               "hipblaslt": lambda a, b, c: blas.gemm(a, b, c, M, N, K, stream=stream)}
+    picks = {"warm": lambda i: (A[0], B[0], C[0]), "c_rotated": lambda i: (A[0], B[0], C[i % n]),
+             "ab_rotated": lambda i: (A[i % n], B[i % n], C[0]), "all_rotated": lambda i: (A[i % n], B[i % n], C[i % n])}
+    out = {"mode": "cold-split", "shape": [M, N, K], "variant": G.variant(idx).label(), "sets": n,
+           "launches_per_window": args.steps, "windows": max(1, args.repeats), "us_per_launch": {}}
+    for kname, fn in kernels.items():
+        for pname, pick in picks.items():
+            count = [0]
+
+            def step():
+                fn(*pick(count[0]))
+                count[0] += 1
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < 1.5:
+                for _ in range(n):
+                    step()
+                torch.cuda.synchronize()
+            _, event_ms = time_windows(step, args.steps, stream, max(1, args.repeats))
+            out["us_per_launch"]["%s/%s" % (kname, pname)] = round(middle(event_ms) * 1e3, 3)
+    blas.close()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -341,7 +413,7 @@ def main():
     ap.add_argument("--no-blaslt", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--allow-partitioned", action="store_true")
-    ap.add_argument("--mode", default="gemm", choices=["gemm", "copy"])
+    ap.add_argument("--mode", default="gemm", choices=["gemm", "copy", "cold-split"])
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -354,6 +426,10 @@ def main():
         raise SystemExit("bench.py needs a GPU")
     if args.mode == "copy":
         run_copy_mode(max(args.steps, 1))
+        return
+    if args.mode == "cold-split":
+        device_check(args.allow_partitioned)
+        run_cold_split(args)
         return
     device = device_check(args.allow_partitioned)
 
