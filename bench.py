@@ -18,8 +18,10 @@ the middle window, with the fastest and slowest windows in `spread`. The same
 launches are also bracketed by HIP events on the launch stream for the roofline
 figure. The hipBLASLt comparator (best of its heuristic candidates, best of a
 before and an after reading, as the reference does in
-bench/check-gemm.cu:357-391) is timed the same way and compared on the same basis
-(wall clock warm, HIP events cold). Prints ONE JSON line.
+bench/check-gemm.cu:357-391) and ours are compared on one basis: HIP events over
+--repeats windows of max(K, 200) launches, warm and cold alike (hipBLASLt's host
+time per call is close to one launch, and a short window would time the host).
+Prints ONE JSON line.
 
 cold: the same launches (ours and hipBLASLt's) rotated over enough operand sets
 that twice the 256 MB MALL is touched between two uses of one set, so every
@@ -160,6 +162,11 @@ def roofline(M, N, K, per_launch_ms, traffic):
 
 # Infinity Cache (MALL) of MI355X: 256 MB, shared by all XCDs in front of HBM.
 MALL_BYTES = 256 << 20
+# Launches per window for the comparisons with hipBLASLt (warm and cold). Its
+# calls go through ctypes and hipblasLtMatmul, whose host time per call is close
+# to a 4096^3 launch; over a short window the GPU then waits on the host and the
+# window times the host. Two hundred launches keep both queues ahead of the GPU.
+COMPARE_LAUNCHES = 200
 WHOLE_DEVICE_CUS = 256
 
 
@@ -350,7 +357,7 @@ def run_copy_mode(steps):
 
 def run_cold_split(args):
     """Which operand's cold lines cost a launch: the GEMM (and hipBLASLt) timed
-    over 7 operand sets with only C rotated, only A and B rotated, or all three,
+    over 7 operand sets with only C, only A, only B, A and B, or all three rotated,
     against one re-used set. Each figure is the middle of --repeats windows of
     --steps launches after 1.5 s of the same rotation. Prints one JSON line (a
     diagnostic, not the metric)."""
@@ -366,16 +373,22 @@ def run_cold_split(args):
     B = [torch.empty((K, N), dtype=torch.float16, device="cuda:0") for _ in range(n)]
     C = [torch.empty((M, N), dtype=torch.float16, device="cuda:0") for _ in range(n)]
     for i in range(n):
-        G.fill_uniform(A[i], 1 + 2 * i)
-        G.fill_uniform(B[i], 2 + 2 * i)
+        if args.operands == "uniform":
+            G.fill_uniform(A[i], 1 + 2 * i)
+            G.fill_uniform(B[i], 2 + 2 * i)
+        else:
+            A[i].fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
+            B[i].fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
     torch.cuda.synchronize()
     blas = G.BlasLt()
     blas.prepare(A[0], B[0], C[0], M, N, K, candidates=16, iters=20, stream=stream)
     kernels = {"ridge": lambda a, b, c: G.launch(idx, a, b, c, M, N, K, stream),
                "hipblaslt": lambda a, b, c: blas.gemm(a, b, c, M, N, K, stream=stream)}
     picks = {"warm": lambda i: (A[0], B[0], C[0]), "c_rotated": lambda i: (A[0], B[0], C[i % n]),
+             "a_rotated": lambda i: (A[i % n], B[0], C[0]), "b_rotated": lambda i: (A[0], B[i % n], C[0]),
              "ab_rotated": lambda i: (A[i % n], B[i % n], C[0]), "all_rotated": lambda i: (A[i % n], B[i % n], C[i % n])}
     out = {"mode": "cold-split", "shape": [M, N, K], "variant": G.variant(idx).label(), "sets": n,
+           "operands": args.operands,
            "launches_per_window": args.steps, "windows": max(1, args.repeats), "us_per_launch": {}}
     for kname, fn in kernels.items():
         for pname, pick in picks.items():
@@ -476,6 +489,7 @@ def main():
             step()
         torch.cuda.synchronize()
     repeats = max(1, args.repeats)
+    compare_steps = max(args.steps, COMPARE_LAUNCHES)
 
     blas = None
     blas_before = blas_after = None
@@ -495,7 +509,7 @@ def main():
 
         for _ in range(args.warmup):
             blas_step()
-        blas_before, _ = time_windows(blas_step, args.steps, stream, repeats)
+        _, blas_before = time_windows(blas_step, compare_steps, stream, repeats)
 
     # The timed region proper: W untimed steps, then `repeats` windows of exactly
     # K steps, each bracketed by torch.cuda.synchronize(); `value` is the middle
@@ -508,7 +522,10 @@ def main():
     per_launch_ms = middle(event_ms)
 
     if blas is not None:
-        blas_after, _ = time_windows(blas_step, args.steps, stream, repeats)
+        # Ours on the comparison's own basis (HIP events, windows of
+        # compare_steps launches), between hipBLASLt's two readings.
+        _, ours_compare = time_windows(step, compare_steps, stream, repeats)
+        _, blas_after = time_windows(blas_step, compare_steps, stream, repeats)
         blas.close()
 
     # Cold: the same launches rotated over operand sets that together exceed
@@ -534,7 +551,7 @@ def main():
                     raise SystemExit("ridge_gemm_launch returned %d" % rc)
             return f
 
-        cold_steps = max(args.steps // 4, 4 * n_sets)
+        cold_steps = max(args.steps // 4, 4 * n_sets, COMPARE_LAUNCHES // 2)
         cold_warm_s = max(0.0, min(args.cold_warm_seconds, args.warm_seconds))
         cold_windows = time_cold(make_step, sets, cold_steps, stream, repeats, cold_warm_s)
         cold_ms = middle(cold_windows)
@@ -591,15 +608,19 @@ def main():
     if blas_error is not None:
         out["hipblaslt"] = {"error": blas_error}
     if blas_before is not None:
-        # Same basis as `value`: the middle window's wall-clock rate, best of the
-        # readings before and after ours (bench/check-gemm.cu:357-391).
+        # Both sides on one basis: HIP events over windows of compare_steps
+        # launches, middle window; hipBLASLt is the better of its readings
+        # before and after ours (bench/check-gemm.cu:357-391).
         before = flops / (middle(blas_before) * 1e-3) / 1e12
         after = flops / (middle(blas_after) * 1e-3) / 1e12
         best = max(before, after)
+        ours = flops / (middle(ours_compare) * 1e-3) / 1e12
         out["hipblaslt"] = {"tflops": round(best, 3), "before": round(before, 3), "after": round(after, 3),
                             "drift": round(abs(after - before) / before, 4),
                             "spread": window_summary(flops, blas_before if before >= after else blas_after),
-                            "frac_of_hipblaslt": round(value / best, 4)}
+                            "ours_tflops": round(ours, 3),
+                            "basis": "HIP events, %d windows of %d launches, middle window" % (repeats, compare_steps),
+                            "frac_of_hipblaslt": round(ours / best, 4)}
     if cold is not None:
         out["cold"] = cold
     out["device"] = device

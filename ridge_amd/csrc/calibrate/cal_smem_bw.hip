@@ -33,7 +33,7 @@ enum Pattern { kPatA = 0, kPatB = 1, kPatMix = 2, kPatLinear = 3 };
 __device__ __forceinline__ int addrA(int lane, int j) {
     const int tm = j % 4, ks = j / 4;  // 4 row tiles x 4 k-steps of a BK = 64 tile
     const int row = tm * 32 + lane % 32;
-    return kAOffset + ridge::swizzleA(row * 8 + 2 * (ks % 4) + lane / 32) * 16;
+    return kAOffset + ridge::swizzleA<8>(row * 8 + 2 * (ks % 4) + lane / 32) * 16;
 }
 
 __device__ __forceinline__ int addrB(int lane, int j) {

@@ -41,7 +41,7 @@ def test_table_has_24_registered_rows_with_consistent_fields():
     keys = [v.key() for v in vs]
     assert len(set(keys)) == 24
     for v in vs:
-        assert v.BM in (64, 128, 256) and v.BN in (64, 128, 256) and v.BK in (32, 64)
+        assert v.BM in (64, 128, 256) and v.BN in (64, 128, 256) and v.BK in (32, 64, 128)
         compute_waves = (v.BM // v.WM) * (v.BN // v.WN)
         ring = v.stages * (v.BM * v.BK + v.BK * v.BN) * 2
         assert v.schedule in (0, 1, 2)

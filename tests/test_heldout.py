@@ -14,13 +14,19 @@ MEASURED = os.path.join(ROOT, "data", "measured", "mi355x-heldout.csv")
 REGISTERED = os.path.join(ROOT, "data", "sweep", "mi355x-heldout-registered.csv")
 FROZEN = os.path.join(ROOT, "data", "sweep", "mi355x-heldout-hw.json")
 IN_SAMPLE = os.path.join(ROOT, "data", "sweep", "mi355x-registered.csv")
+# The kernel table at the registration commit; the held-out cross product is
+# shapes x these rows, whatever the table holds now.
+TABLE = os.path.join(ROOT, "data", "sweep", "mi355x-heldout-table.csv")
 
 
 def test_heldout_shapes_are_disjoint_from_the_sweep_and_fully_measured():
     held = [s[:3] for s in T.read_shapes(REGISTERED)]
     assert len(held) == 14 and not set(held) & {s[:3] for s in T.read_shapes(IN_SAMPLE)}
     table = T.read(MEASURED)
-    absent, unexpected = V.registered_gate(table.records, T.read_shapes(REGISTERED), V.kernel_table_keys())
+    frozen = T.read(TABLE, require=V.KEY_COLUMNS)
+    keys = [tuple(frozen.number(i, c, int) for c in V.KEY_COLUMNS) for i in range(len(frozen))]
+    assert len(set(keys)) == 24
+    absent, unexpected = V.registered_gate(table.records, T.read_shapes(REGISTERED), keys)
     assert not absent and not unexpected
     assert float(table.meta["canary_drift_fraction"]) <= 0.05
 
