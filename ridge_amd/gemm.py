@@ -185,6 +185,20 @@ def launch(i, A, B, C, M, N, K, stream=None):
     return lib().ridge_gemm_launch(i, _ptr(A), _ptr(B), _ptr(C), M, N, K, _stream_handle(stream))
 
 
+def bound_launch(i, A, B, C, M, N, K, stream=None):
+    """A zero-argument callable that enqueues C = A B with variant i, its
+    arguments converted once: the per-call host cost is one foreign call, for
+    timing loops whose launches are shorter than Python's argument handling."""
+    f = lib().ridge_gemm_launch
+    args = (i, _ptr(A), _ptr(B), _ptr(C), M, N, K, _stream_handle(stream))
+
+    def call():
+        rc = f(*args)
+        if rc != HIP_SUCCESS:
+            raise RidgeGemmError("ridge_gemm_launch(variant %d, %dx%dx%d) returned hipError %d" % (i, M, N, K, rc))
+    return call
+
+
 def _check_operands(A, B, C=None):
     import torch
     if A.dtype != torch.float16 or B.dtype != torch.float16:
@@ -250,6 +264,17 @@ class BlasLt:
                                      _stream_handle(stream))
         if rc != 0:
             raise RidgeGemmError("ridge_blaslt_gemm(%dx%dx%d) returned %d" % (M, N, K, rc))
+
+    def bound_gemm(self, A, B, C, M, N, K, c_is_f32=False, stream=None):
+        """gemm() as a zero-argument callable with its arguments converted once."""
+        f = lib().ridge_blaslt_gemm
+        args = (self._h, _ptr(A), _ptr(B), _ptr(C), M, N, K, int(c_is_f32), _stream_handle(stream))
+
+        def call():
+            rc = f(*args)
+            if rc != 0:
+                raise RidgeGemmError("ridge_blaslt_gemm(%dx%dx%d) returned %d" % (M, N, K, rc))
+        return call
 
     def close(self):
         if self._h:
