@@ -101,6 +101,18 @@ struct HardwareModel {
     double mallRefillBytesPerSec = 0.0;  // [CAL] rate of the L2-missing refill path (cal-smem-bw)
     double mallStretchLoad[5] = {0.0, 0.0, 0.0, 0.0, 0.0};  // [CAL] path load at miss share 0..1
     double mallStretch[5] = {0.0, 0.0, 0.0, 0.0, 0.0};      // [CAL] the skeleton K-step's stretch there
+    int persistentStepModel = 0;     // 0: a persistent row's K-step is the uniform schedule's (reference:
+                                     //    no persistent rows)
+                                     // 1: its K-step is (reads + MFMAs) scaled by what the persistent
+                                     //    skeleton measures for the same class of row: the measured
+                                     //    cycles per K tile over the model's reads + MFMAs for the
+                                     //    skeleton's row (128x128x64 w64x64 s4 with one compute wave
+                                     //    per SIMD, 256x128x32 w64x64 s6 with two)
+    double persistentStepCycles[2] = {0.0, 0.0};  // [CAL] cycles per K tile of those two skeletons
+    int fillShareModel = 0;          // 0: every workgroup fetches its first tiles from HBM (reference)
+                                     // 1: the resident workgroups' first tiles come from HBM once per
+                                     //    distinct panel an XCD holds (the kernels' launch order) and
+                                     //    from the L2s for the rest, at l2HitBytesPerCycle
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -107,6 +107,13 @@ def band_check(res, spec):
     if "fillLatencySec" in res:
         ok &= check("fillLatencySec", res["fillLatencySec"] * 1e6, 0.2, 10.0, "us",
                     "first-tile wait of a whole grid from HBM")
+    for i in (1, 2):
+        key = "persistentStepCycles%d" % i
+        if key in res and "pingPongMfmaCycles" in res:
+            # Both persistent skeletons issue 32 MFMAs per SIMD per K tile, half
+            # the ping-pong skeleton's K-step, and at best hide their reads.
+            ok &= check(key, res[key], 0.45 * res["pingPongMfmaCycles"], 2.0 * res["pingPongMfmaCycles"], "cycles",
+                        "persistent skeleton K tile: at least its MFMAs")
     if "mallRefillBytesPerSec" in res:
         ok &= check("mallRefillBytesPerSec", res["mallRefillBytesPerSec"] / 1e12, 1.0,
                     res["l2HitBytesPerCycle"] * res["clockHz"] / 1e12, "TB/s",
@@ -200,17 +207,20 @@ def hardware_json(res, spec, arch):
         "freeRunningOverlap": res["freeRunningOverlap"],
         "powerModel": 1,
         "loadedClockRatio": loaded_clock_ratio(res),
+        "fillShareModel": 1,
     }
     for key in CLOCK_RATIO_KEYS:
         out[key] = res[key]
     # Constants of the later calibration benches, written (with the model term
     # that reads them switched on) when the log has them.
-    for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec"] +
+    for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec", "persistentStepCycles1",
+                 "persistentStepCycles2"] +
                 ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
         if key in res:
             out[key] = res[key]
     for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]), ("fillLatencyModel", ["fillLatencySec"]),
-                        ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)])):
+                        ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)]),
+                        ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"])):
         if all(k in res for k in needs):
             out[term] = 1
     for key in SKELETON_KEYS:

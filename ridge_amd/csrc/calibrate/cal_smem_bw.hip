@@ -12,7 +12,8 @@
 //        ceiling the others are checked against
 // Loads are kept in the loop by a compiler memory barrier per iteration and their
 // results are folded into a value that is stored only under an impossible
-// condition.
+// condition. The ping-pong and persistent skeletons further down time the two
+// schedules' K-steps for the model's overlap, power, MALL and persistent terms.
 #include "cal_common.hpp"
 #include "gemm_mfma.hpp"
 
@@ -233,6 +234,182 @@ double pingPongCycles(int cus, const uint32_t* dOperands, const char* dRefill, c
     return cyc / kIters;
 }
 
+// The persistent schedule's main loop for one table row (gemmMfmaPersistentKernel
+// without its tile walk and epilogue): compute waves 0 .. kWaves-1 run the
+// kernel's k-steps (fragments double-buffered, MFMAs interleaved with the next
+// k-step's reads, one barrier per K tile); the two loader waves refill the ring
+// with the kernel's direct-to-LDS loads and swizzled lane offsets, from a
+// four-tile L2-resident source. G K tiles per launch. Modes: 0 both halves of a
+// k-step, 1 the fragment reads alone, 2 the MFMAs alone (on fragments read once).
+// Every wave passes G barriers, as in the kernel.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int Mode>
+__global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders) * 64) void persistentSkeletonKernel(
+    const _Float16* src, int G, float* sink, Stamp* out) {
+    using T = ridge::GemmTraits<BM, BN, BK, WM, WN, STAGES, 8>;
+    using P = ridge::PersistentTraits<BM, BN, BK, WM, WN, STAGES, 8>;
+    using Blk = ridge::GemmBlock<BM, BN, BK, WM, WN, STAGES, 8>;
+    constexpr int TM = T::kTilesM;
+    constexpr int TN = T::kTilesN;
+    constexpr int KS = T::kSteps;
+    constexpr int L = P::kLoads;
+    constexpr int kTileBytes = T::kBytesA + T::kBytesB;
+    __shared__ __attribute__((aligned(1024))) char lds[P::kLdsBytes];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64;
+    const uint64_t c0 = cycles();
+    const uint64_t r0 = realtime();
+    if (wave >= T::kWaves) {
+        // The source holds four K tiles, each an A tile (BM rows of BK halves)
+        // followed by a B tile (BK rows of BN halves), rows contiguous.
+        const int l = wave - T::kWaves;
+        const uint32_t ldsBase = ridge::ldsAddress(lds);
+        uint32_t offA[P::kLoadsA], offB[P::kLoadsB];
+#pragma unroll
+        for (int i = 0; i < P::kLoadsA; ++i) {
+            const int q = ridge::swizzleA<T::kChunksPerRowA>((i * P::kLoaders + l) * 64 + lane);
+            offA[i] = (uint32_t)(((q / T::kChunksPerRowA) * BK + (q % T::kChunksPerRowA) * 8) * 2);
+        }
+#pragma unroll
+        for (int i = 0; i < P::kLoadsB; ++i) {
+            const int q = ridge::swizzleB<T::kChunksPerRowB>((i * P::kLoaders + l) * 64 + lane);
+            offB[i] = (uint32_t)(T::kBytesA + ((q / T::kChunksPerRowB) * BN + (q % T::kChunksPerRowB) * 8) * 2);
+        }
+        auto issue = [&](int g, int stage) {
+            uint32_t lb = ldsBase;
+            asm volatile("" : "+s"(lb));
+            const char* base = reinterpret_cast<const char*>(src) + (g & 3) * kTileBytes;
+#pragma unroll
+            for (int i = 0; i < P::kLoadsA; ++i)
+                ridge::globalLoadLds16(base, offA[i], lb + stage * T::kBytesA + (i * P::kLoaders + l) * 1024);
+#pragma unroll
+            for (int i = 0; i < P::kLoadsB; ++i)
+                ridge::globalLoadLds16(base, offB[i],
+                                       lb + T::kRegionA + stage * T::kBytesB + (i * P::kLoaders + l) * 1024);
+        };
+        ridge::staticFor<STAGES - 1>([&](auto sC) {
+            if (sC.value < G) issue(sC.value, sC.value);
+        });
+        if (G >= STAGES - 1) {
+            ridge::waitVmcnt<(STAGES - 2) * L>();
+        } else {
+            ridge::waitVmcnt<0>();
+        }
+        ridge::barrierLds();  // B_0
+        for (int g0 = 0; g0 < G; g0 += STAGES) {
+            ridge::staticFor<STAGES>([&](auto sC) {
+                constexpr int s = sC.value;
+                const int g = g0 + s;
+                if (g + 1 < G) {
+                    if (g + STAGES - 1 < G) {
+                        issue(g + STAGES - 1, (s + STAGES - 1) % STAGES);
+                        ridge::waitVmcnt<(STAGES - 2) * L>();
+                    } else {
+                        ridge::waitVmcnt<0>();
+                    }
+                    ridge::barrierLds();  // B_{g+1}
+                }
+            });
+        }
+        return;
+    }
+    // One column of tiles, one per workgroup: the block only forms its LDS
+    // fragment offsets here and never touches global memory.
+    Blk blk(lds, src, src, BM * (int)gridDim.x, BN, BK * G);
+    ridge::barrierLds();  // B_0
+    half8_t fa[2][TM];
+    half8_t fb[2][TN];
+    blk.template readFrags<0>(0, fa[0], fb[0]);
+    blk.template readFrags<0>(0, fa[1], fb[1]);
+    constexpr int U = (STAGES * KS) % 2 == 0 ? STAGES : 2 * STAGES;
+    for (int g0 = 0; g0 < G; g0 += U) {
+        ridge::staticFor<U>([&](auto iC) {
+            constexpr int i = iC.value;
+            constexpr int s = i % STAGES;
+            constexpr int sNext = (s + 1) % STAGES;
+            const int g = g0 + i;
+            if (g < G) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int cur = (i * KS + ks) & 1;
+                    if (ks + 1 < KS) {
+                        if (Mode != 2) blk.template readFrags<s>(ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                    } else if (g + 1 < G) {
+                        ridge::barrierLds();  // B_{g+1}
+                        if (Mode != 2) blk.template readFrags<sNext>(0, fa[cur ^ 1], fb[cur ^ 1]);
+                    }
+                    if (Mode != 1) {
+                        blk.mfmaStep(fa[cur], fb[cur]);
+                        ridge::interleaveHint<TM, TN>();
+                    } else {
+                        // Consume the fragments at no instruction cost.
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm) asm volatile("" ::"v"(fa[cur][tm]));
+#pragma unroll
+                        for (int tn = 0; tn < TN; ++tn) asm volatile("" ::"v"(fb[cur][tn]));
+                    }
+                }
+            }
+        });
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const uint64_t c1 = cycles();
+    const uint64_t r1 = realtime();
+    float acc = 0.0f;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc += blk.acc[tm][tn][0] + blk.acc[tm][tn][3];
+    if (acc == -1.0e38f) sink[0] = acc;
+    if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
+}
+
+constexpr int kPersistentTiles = 1024;  // K tiles per skeleton launch
+
+// Median cycles per K tile of the persistent skeleton over every CU (one
+// workgroup each), and the median clock.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int Mode>
+double persistentCycles(int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, double& clockHz) {
+    using P = ridge::PersistentTraits<BM, BN, BK, WM, WN, STAGES, 8>;
+    auto k = persistentSkeletonKernel<BM, BN, BK, WM, WN, STAGES, Mode>;
+    hipLaunchKernelGGL(k, dim3(cus), dim3(P::kThreads), 0, nullptr, dSrc, kPersistentTiles, dSink, dStamps);
+    CAL_HIP_CHECK(hipGetLastError());
+    CAL_HIP_CHECK(hipDeviceSynchronize());
+    std::vector<Stamp> st(cus);
+    CAL_HIP_CHECK(hipMemcpy(st.data(), dStamps, cus * sizeof(Stamp), hipMemcpyDeviceToHost));
+    double cyc = 0.0;
+    medianStamps(st, cyc, clockHz);
+    return cyc / kPersistentTiles;
+}
+
+// One persistent row's cycles per K tile (the median of kRepeats launches),
+// reported as `key`; beside it the reads and the MFMAs alone and the share of
+// the shorter of the two that the row's waves hide under the longer,
+// (t_reads + t_MFMAs - t_both) / min(t_reads, t_MFMAs), as a record.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+double persistentStep(const char* key, int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, bool& ok) {
+    std::vector<double> both, reads, mfma;
+    double hz = 0.0, hzBoth = 0.0;
+    for (int r = 0; r < kRepeats; ++r) {
+        both.push_back(persistentCycles<BM, BN, BK, WM, WN, STAGES, 0>(cus, dSrc, dSink, dStamps, hzBoth));
+        reads.push_back(persistentCycles<BM, BN, BK, WM, WN, STAGES, 1>(cus, dSrc, dSink, dStamps, hz));
+        mfma.push_back(persistentCycles<BM, BN, BK, WM, WN, STAGES, 2>(cus, dSrc, dSink, dStamps, hz));
+    }
+    const double tBoth = middle(both), tReads = middle(reads), tMfma = middle(mfma);
+    const double hidden = (tReads + tMfma - tBoth) / std::min(tReads, tMfma);
+    std::printf("  %dx%dx%d w%dx%d s%d (%d compute waves): both %.1f, reads %.1f, MFMAs %.1f cycles per K tile "
+                "at %.1f MHz; hidden share %.3f\n",
+                BM, BN, BK, WM, WN, STAGES, (BM / WM) * (BN / WN), tBoth, tReads, tMfma, hzBoth / 1e6, hidden);
+    ok &= reportConstant(key, tBoth, "cycles", both);
+    // The reads alone share LDS with the loaders' refill and spread more from
+    // launch to launch; they are a record, not a constant, so 10% is the limit.
+    ok &= reportConstant("persistentReadCycles", tReads, "cycles", reads, 0.10);
+    ok &= reportConstant("persistentMfmaCycles", tMfma, "cycles", mfma);
+    std::printf("CAL_INFO %sHiddenShare %.6f\n", key, hidden);
+    std::printf("CAL_INFO %sClockHz %.6e\n", key, hzBoth);
+    std::printf("CAL_RESULT %s %.6f\n", key, tBoth);
+    return tBoth;
+}
+
 // U[-1,1) halves from splitmix64, packed two per word: 16 KiB.
 std::vector<uint32_t> randomHalfWords() {
     std::vector<uint32_t> w(16 * 1024 / 4);
@@ -418,6 +595,21 @@ int main() {
     // queue on it and spread more from launch to launch; their limit is 20%.
     for (int m = 0; m < kModes; ++m)
         ok &= reportConstant(kModeKeys[m], tStep[m], "cycles", st[m], (m == 6 || m == 8) ? 0.20 : 0.05);
+
+    // The persistent schedule's skeletons: one row with one compute wave per
+    // SIMD (128x128x64 w64x64 s4) and one with two (256x128x32 w64x64 s6).
+    // Source: four K tiles of U[-1,1) halves (the operand block, repeated).
+    std::printf("\npersistent skeleton: compute waves + 2 loader waves, one barrier per K tile, %d K tiles\n",
+                kPersistentTiles);
+    _Float16* dSrc = nullptr;
+    constexpr size_t kSrcBytes = 4 * 48 * 1024;
+    CAL_HIP_CHECK(hipMalloc(&dSrc, kSrcBytes));
+    for (size_t off = 0; off < kSrcBytes; off += 16 * 1024)
+        CAL_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(dSrc) + off, hOperands.data(), 16 * 1024,
+                                hipMemcpyHostToDevice));
+    persistentStep<128, 128, 64, 64, 64, 4>("persistentStepCycles1", cus, dSrc, dFSink, dStamps, ok);
+    persistentStep<256, 128, 32, 64, 64, 6>("persistentStepCycles2", cus, dSrc, dFSink, dStamps, ok);
+    CAL_HIP_CHECK(hipFree(dSrc));
     CAL_HIP_CHECK(hipFree(dOperands));
     CAL_HIP_CHECK(hipFree(dRefill));
     CAL_HIP_CHECK(hipFree(dFSink));

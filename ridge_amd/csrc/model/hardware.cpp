@@ -118,7 +118,9 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("mallStretchLoad2", h.mallStretchLoad[2]), R("mallStretchLoad3", h.mallStretchLoad[3]),
         R("mallStretchLoad4", h.mallStretchLoad[4]), R("mallStretch0", h.mallStretch[0]),
         R("mallStretch1", h.mallStretch[1]), R("mallStretch2", h.mallStretch[2]), R("mallStretch3", h.mallStretch[3]),
-        R("mallStretch4", h.mallStretch[4]),
+        R("mallStretch4", h.mallStretch[4]), I("persistentStepModel", h.persistentStepModel),
+        R("persistentStepCycles1", h.persistentStepCycles[0]), R("persistentStepCycles2", h.persistentStepCycles[1]),
+        I("fillShareModel", h.fillShareModel),
     };
 }
 
@@ -177,6 +179,10 @@ std::string inconsistency(const HardwareModel& h) {
         return "hbmWriteModel 1 reads hbmWriteBytesPerSec, which must be positive";
     if (h.fillLatencyModel == 1 && !(h.fillLatencySec > 0.0))
         return "fillLatencyModel 1 reads fillLatencySec, which must be positive";
+    if (h.fillShareModel == 1 && !(h.l2HitBytesPerCycle > 0.0))
+        return "fillShareModel 1 reads l2HitBytesPerCycle, which must be positive";
+    if (h.persistentStepModel == 1 && !(h.persistentStepCycles[0] > 0.0 && h.persistentStepCycles[1] > 0.0))
+        return "persistentStepModel 1 reads persistentStepCycles1 and persistentStepCycles2, which must be positive";
     return "";
 }
 

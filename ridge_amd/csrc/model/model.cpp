@@ -52,6 +52,14 @@
 //   write stream          = hw.hbmWriteModel 1: C is written at the calibrated
 //                           streaming-write rate, A and B read at the read rate,
 //                           and the two times add (reference: one DRAM rate)
+//   shared fill           = hw.fillShareModel 1: the resident tiles' first K
+//                           tiles cross from HBM once per distinct panel of an
+//                           XCD (the launch order) and come from the L2s for
+//                           the rest (reference: every workgroup from HBM)
+//   persistent K-step     = hw.persistentStepModel 1: a persistent row's reads +
+//                           MFMAs scaled by the measured/modelled ratio of the
+//                           persistent skeleton of its class (one or two compute
+//                           waves per SIMD) (reference: no persistent rows)
 //   persistent rows       = hw.persistentModel 1 and cfg.schedule 2: two loader
 //                           waves and the epilogue staging join the workgroup,
 //                           which walks ceil(tiles / slots) tiles and pays one
@@ -181,6 +189,39 @@ void launchOrderPanels(const GemmConfig& cfg, const HardwareModel& hw, long long
     }
 }
 
+// Per K-step cycles of one workgroup's matrix instructions and of the operand
+// reads out of LDS that feed them (for cfg's wave grid and BK).
+void stepParts(const GemmConfig& cfg, const HardwareModel& hw, int db, double& tCompute, double& tSmem) {
+    const int numWarps = (cfg.BM / cfg.warpM) * (cfg.BN / cfg.warpN);
+    const double mmasPerWarpPerStep =
+        double(cfg.warpM / cfg.mmaM) * (cfg.warpN / cfg.mmaN) * (cfg.BK / cfg.mmaK);
+    tCompute = mmasPerWarpPerStep * numWarps * hw.mmaCyclesPerInst;
+    const double smemBytesPerStep = double(numWarps) * (cfg.warpM + cfg.warpN) * cfg.BK * db;
+    // ldsReadModel 1: A fragments come from ds_read_b128, B fragments from the
+    // transposing ds_read_b64_tr_b16 at half its rate; each at its calibrated rate.
+    tSmem = hw.ldsReadModel == 1
+                ? double(numWarps) * cfg.BK * db *
+                      (cfg.warpM / hw.ldsAReadBytesPerCycle + cfg.warpN / hw.ldsBTrReadBytesPerCycle)
+                : smemBytesPerStep / hw.smemBytesPerCycle;
+}
+
+// persistentStepModel 1: the measured K-step of the persistent skeleton of a
+// row's class over the model's reads + MFMAs for the skeleton's own row. The
+// skeletons are cal-smem-bw's: 128x128x64 w64x64 (one compute wave per SIMD)
+// and 256x128x32 w64x64 (two).
+double persistentStepRatio(const GemmConfig& cfg, const HardwareModel& hw, int db, int computeWavesPerSimd) {
+    GemmConfig skel = cfg;
+    const bool two = computeWavesPerSimd >= 2;
+    skel.BM = two ? 256 : 128;
+    skel.BN = 128;
+    skel.BK = two ? 32 : 64;
+    skel.warpM = 64;
+    skel.warpN = 64;
+    double tC = 0.0, tS = 0.0;
+    stepParts(skel, hw, db, tC, tS);
+    return hw.persistentStepCycles[two ? 1 : 0] / (tC + tS);
+}
+
 }  // namespace
 
 Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
@@ -207,16 +248,8 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // reads out of LDS that feed them (in series: the next instruction consumes
     // the registers the read just wrote). The global->LDS copies are
     // asynchronous and appear only in the envelope.
-    const double mmasPerWarpPerStep =
-        double(cfg.warpM / cfg.mmaM) * (cfg.warpN / cfg.mmaN) * (cfg.BK / cfg.mmaK);
-    const double tCompute = mmasPerWarpPerStep * numWarps * hw.mmaCyclesPerInst;
-    const double smemBytesPerStep = double(numWarps) * (cfg.warpM + cfg.warpN) * cfg.BK * db;
-    // ldsReadModel 1: A fragments come from ds_read_b128, B fragments from the
-    // transposing ds_read_b64_tr_b16 at half its rate; each at its calibrated rate.
-    const double tSmem = hw.ldsReadModel == 1
-                             ? double(numWarps) * cfg.BK * db *
-                                   (cfg.warpM / hw.ldsAReadBytesPerCycle + cfg.warpN / hw.ldsBTrReadBytesPerCycle)
-                             : smemBytesPerStep / hw.smemBytesPerCycle;
+    double tCompute = 0.0, tSmem = 0.0;
+    stepParts(cfg, hw, db, tCompute, tSmem);
     // The ping-pong schedule (two waves per SIMD, a ring of three or more stages)
     // runs one wave's operand reads under the other wave's MFMAs, so a K-step
     // costs the longer of the two instead of their sum.
@@ -228,8 +261,14 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // whose compute waves run the same loop with one barrier per K tile) hide
     // part of the shorter phase under the longer with no schedule doing it: the
     // share cal-smem-bw measures for the same waves without barriers.
-    if (!pingPong && hw.uniformOverlapModel == 1 && hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM)
+    if (persistent && hw.persistentStepModel == 1 && hw.simdsPerSM > 0) {
+        // The persistent skeleton of the row's class has the row's barriers,
+        // loader waves and refill; its measured K-step replaces the overlap
+        // share of barrier-free waves.
+        tStep = persistentStepRatio(cfg, hw, db, numWarps / hw.simdsPerSM) * (tCompute + tSmem);
+    } else if (!pingPong && hw.uniformOverlapModel == 1 && hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM) {
         tStep -= hw.freeRunningOverlap * std::min(tCompute, tSmem);
+    }
     p.tComputeCycles = tCompute;
     p.tSmemCycles = tSmem;
     p.tStepCycles = tStep;
@@ -329,7 +368,21 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
     // only the tiles that exist (prologueModel 1).
     const double prologueTiles =
         hw.prologueModel == 1 ? std::min(double(cfg.stages - 1), kSteps) : double(cfg.stages - 1);
-    const double tPrologue = prologueTiles * tileBytes / gmemBytesPerCycle / ctasPerSM;
+    double tPrologue = prologueTiles * tileBytes / gmemBytesPerCycle / ctasPerSM;
+    if (hw.fillShareModel == 1) {
+        // The resident workgroups fill together. Each XCD fetches each distinct
+        // A row panel and B column panel slice of its tiles from HBM once; the
+        // other workgroups sharing that slice read it from the XCD's L2. The
+        // fill takes that split's time instead of every tile's bytes from HBM.
+        const long long n = (long long)std::min(ctaSlots, totalCtas);
+        double rowPanels = 0.0, colPanels = 0.0;
+        launchOrderPanels(cfg, hw, n, rowPanels, colPanels);
+        const double allBytes = double(n) * tileBytes;
+        const double uniqueBytes = std::min(allBytes, (rowPanels * cfg.BM + colPanels * cfg.BN) * double(cfg.BK) * db);
+        const double shared =
+            uniqueBytes / hw.hbmBytesPerSec + (allBytes - uniqueBytes) / (hw.l2HitBytesPerCycle * hw.clockHz);
+        tPrologue *= std::min(1.0, shared / (allBytes / hw.hbmBytesPerSec));
+    }
     // hbmWriteModel 1: the drain moves at the streaming-write rate.
     const double drainBytesPerCycle =
         hw.hbmWriteModel == 1 ? hw.hbmWriteBytesPerSec / (hw.clockHz * double(hw.numSMs)) : gmemBytesPerCycle;

@@ -86,15 +86,16 @@ def main(argv=None):
     ap.add_argument("--out", default="data/sweep/mi355x-registered.csv")
     ap.add_argument("--baseline-out", default="data/sweep/mi355x-baseline-configs.csv")
     ap.add_argument("--tag-prefix", default="s", help="first letter(s) of every shape tag")
-    ap.add_argument("--exclude", default=None,
-                    help="a registered sweep whose shapes this one must not repeat (a held-out set)")
+    ap.add_argument("--exclude", action="append", default=[],
+                    help="a registered sweep whose shapes this one must not repeat (a held-out set); repeatable")
     ap.add_argument("--note", action="append", default=[], help="an extra header line")
     args = ap.parse_args(argv)
     os.makedirs(os.path.dirname(args.out) or ".", exist_ok=True)
-    exclude = ()
+    exclude = []
     if args.exclude:
         from ridge_amd import tables as T
-        exclude = [s[:3] for s in T.read_shapes(args.exclude)]
+        for path in args.exclude:
+            exclude += [s[:3] for s in T.read_shapes(path)]
     write_registered(args.out, args.seed, args.tag_prefix, exclude, args.note)
     if args.baseline_out != "-":
         write_baseline(args.baseline_out)

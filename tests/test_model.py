@@ -642,3 +642,69 @@ def test_fill_latency_model_adds_one_wait_per_round(tmp_path):
         assert b["predictedTFLOPS"] == pytest.approx(flops / (flops / (a["predictedTFLOPS"] * 1e12) +
                                                              want_rounds * 1e-6) / 1e12)
         assert b["predictedTFLOPS"] == pytest.approx(min(b["computeTFLOPS"], b["hbmTFLOPS"]))
+
+
+def test_persistent_step_model_scales_by_the_skeleton_of_the_class(tmp_path):
+    """persistentStepModel 1 on the placeholders (4 cycles per MFMA per CU, one
+    blended 128 B/cycle LDS rate). The skeleton rows' own reads + MFMAs:
+      128x128x64 w64x64 (4 waves, one per SIMD): tC = 32 MFMAs x 4 waves x 4 =
+        512, tS = 4 x (64 + 64) x 64 x 2 B / 128 = 512: 1024 cycles;
+      256x128x32 w64x64 (8 waves, two per SIMD): tC = 16 x 8 x 4 = 512,
+        tS = 8 x 128 x 32 x 2 / 128 = 512: 1024 cycles.
+    With measured K tiles of 768 and 896 cycles the ratios are 0.75 and 0.875.
+    A 128x64x64 w64x32 persistent row (one wave per SIMD) has tC = 16 x 4 x 4 =
+    256 and tS = 4 x 96 x 64 x 2 / 128 = 384, so 0.75 x 640 = 480 cycles; the
+    256x128x32 row itself 0.875 x 1024 = 896. One-tile-per-workgroup rows keep
+    their schedule's K-step."""
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % ', "persistentStepModel": 1, "persistentStepCycles1": 768, '
+                                '"persistentStepCycles2": 896')
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % "")
+    hw_on, hw_off = RM.Hardware(str(on)), RM.Hardware(str(off))
+    small = dict(M=8192, N=8192, K=4096, BM=128, BN=64, BK=64, warpM=64, warpN=32, stages=6, regsPerThread=131,
+                 groupM=8, schedule=2)
+    assert RM.predict(hw_off, **small)["tStepCycles"] == pytest.approx(640.0)
+    assert RM.predict(hw_on, **small)["tStepCycles"] == pytest.approx(480.0)
+    skel1 = dict(small, BN=128, warpN=64, stages=4, regsPerThread=185)
+    assert RM.predict(hw_on, **skel1)["tStepCycles"] == pytest.approx(768.0)
+    eight = dict(small, BM=256, BN=128, BK=32, warpM=64, warpN=64, regsPerThread=167, groupM=4)
+    assert RM.predict(hw_off, **eight)["tStepCycles"] == pytest.approx(1024.0)
+    assert RM.predict(hw_on, **eight)["tStepCycles"] == pytest.approx(896.0)
+    uniform = dict(small, schedule=0, stages=3)
+    assert RM.predict(hw_on, **uniform)["tStepCycles"] == RM.predict(hw_off, **uniform)["tStepCycles"]
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "persistentStepModel": 1, "persistentStepCycles1": 768')
+    with pytest.raises(ValueError, match="persistentStepModel 1"):
+        RM.Hardware(str(bad))
+
+
+def test_fill_share_model_fetches_each_panel_slice_once_per_xcd(tmp_path):
+    """fillShareModel 1 with HBM at 8 TB/s and the L2s at 8192 B/cycle x 2.4 GHz
+    = 19.6608 TB/s, on one XCD. 2048 x 2048 x 1024 on 128x128x64 w64x64 s2: two
+    workgroups per CU by LDS (64 KiB rings), so all 256 tiles are resident and the
+    XCD holds 16 row and 16 column panels. A K tile of every resident tile is
+    256 x 32,768 = 8,388,608 B, of which (16 x 128 + 16 x 128) x 64 x 2 = 524,288 B
+    are distinct: 524,288 / 8e12 + 7,864,320 / 19.6608e12 = 0.465536 us against
+    8,388,608 / 8e12 = 1.048576 us, a factor 0.443970 on the fill. The fill is
+    one tile (stages - 1) of 32,768 B at 8e12 / (2.4e9 x 256) = 13.0208 B/cycle
+    per CU, over 2 resident workgroups: 1258.29 cycles, 558.64 with the term."""
+    base = ', "numXcds": 1, "l2HitBytesPerCycle": 8192'
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % base)
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % (base + ', "fillShareModel": 1'))
+    cfg = dict(M=2048, N=2048, K=1024, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128)
+    p_off = RM.predict(RM.Hardware(str(off)), **cfg)
+    p_on = RM.predict(RM.Hardware(str(on)), **cfg)
+    assert p_off["ctasPerSM"] == 2 and p_off["totalCtas"] == 256
+    assert p_off["tPrologueCycles"] == pytest.approx(32768 / (8e12 / (2.4e9 * 256)) / 2)
+    factor = (524288 / 8e12 + 7864320 / (8192 * 2.4e9)) / (8388608 / 8e12)
+    assert factor == pytest.approx(0.443970, abs=1e-6)
+    assert p_on["tPrologueCycles"] == pytest.approx(p_off["tPrologueCycles"] * factor)
+    assert p_on["tPrologueCycles"] == pytest.approx(558.64, abs=0.01)
+    assert p_on["tEpilogueCycles"] == p_off["tEpilogueCycles"]
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "fillShareModel": 1')
+    with pytest.raises(ValueError, match="fillShareModel 1"):
+        RM.Hardware(str(bad))
