@@ -424,14 +424,20 @@ struct GemmBlock {
 
     // One k-step of MFMAs, B fragment in the first operand (transposed C tile).
     // B outer, A inner: consecutive MFMAs share their first operand (measured
-    // slightly faster than sharing the second). Each accumulator still receives
-    // its k contributions in order, so the result does not depend on this order.
+    // slightly faster than sharing the second). The A order snakes (ascending
+    // for even tn, descending for odd), so at each change of B the second
+    // operand stays too: one operand switch fewer per B column, measured
+    // +0.3-0.6% on the power-limited 256x256 rows. Each accumulator still
+    // receives its k contributions in order, so the result does not depend on
+    // this order.
     __device__ __forceinline__ void mfmaStep(const half8_t (&a)[TM], const half8_t (&b)[TN]) {
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm)
+            for (int i = 0; i < TM; ++i) {
+                const int tm = (tn & 1) ? TM - 1 - i : i;
                 acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b[tn], a[tm], acc[tm][tn], 0, 0, 0);
+            }
     }
 
     // Epilogue through LDS (storeStaged below). Regions are per wave, so the
