@@ -118,6 +118,66 @@ def rank_shapes(rows):
     return out
 
 
+@dataclass
+class LaunchOrderSummary:
+    """Rows of one shape that differ only in groupM, compared in pairs.
+
+    `footprint` of a row is the A rows plus B columns that the tiles resident on
+    one XCD touch (reuseTilesM * BM + reuseTilesN * BN, the model's launch-order
+    term): the bytes each XCD pulls per K-step are proportional to it."""
+    families: int
+    violations: int        # pairs whose predictions tie iff their footprints differ
+    equal_pairs: int       # pairs with equal footprints (tied by construction)
+    equal_spread: list     # their measured difference, % of the faster
+    ordered_pairs: int     # pairs with different footprints
+    concordant: int        # ... that the model orders as measured
+    discordant: list       # (shape, (groupM, footprint, predicted, measured) x 2)
+
+
+def launch_order_families(rows, hw_path):
+    """The reference predicts one number for every swizzle setting (README.md:154);
+    here groupM enters through the per-XCD panel count. Checks, over every family
+    of rows that differ only in groupM, that two launch orders tie exactly when
+    their per-XCD footprints are equal, and how often the model orders the others
+    as measured."""
+    hw = RM.Hardware(hw_path)
+    fams = collections.OrderedDict()
+    for j in rows:
+        r = j.record
+        key = tuple(r[c] for c in ("M", "N", "K", "BM", "BN", "BK", "WM", "WN", "stages")) + (r.get("schedule", "-1"),)
+        fams.setdefault(key, []).append(j)
+    out = LaunchOrderSummary(0, 0, 0, [], 0, 0, [])
+    for key, js in fams.items():
+        if len(js) < 2:
+            continue
+        out.families += 1
+        members = []
+        for j in js:
+            r = j.record
+            p = RM.predict(hw, M=int(r["M"]), N=int(r["N"]), K=int(r["K"]), BM=int(r["BM"]), BN=int(r["BN"]),
+                           BK=int(r["BK"]), warpM=int(r["WM"]), warpN=int(r["WN"]), stages=int(r["stages"]),
+                           regsPerThread=int(r["regsPerThread"]), groupM=int(r["groupM"]),
+                           schedule=int(r.get("schedule", "-1") or -1))
+            footprint = p["reuseTilesM"] * int(r["BM"]) + p["reuseTilesN"] * int(r["BN"])
+            members.append((int(r["groupM"]), footprint, p["predictedTFLOPS"], j.measured))
+        for a in range(len(members)):
+            for b in range(a + 1, len(members)):
+                x, y = members[a], members[b]
+                if (x[1] == y[1]) != (x[2] == y[2]):
+                    out.violations += 1
+                if x[1] == y[1]:
+                    out.equal_pairs += 1
+                    out.equal_spread.append(abs(x[3] - y[3]) / max(x[3], y[3]) * 100.0)
+                    continue
+                out.ordered_pairs += 1
+                if (x[2] - y[2]) * (x[3] - y[3]) > 0:
+                    out.concordant += 1
+                else:
+                    out.discordant.append((key[:3], x, y))
+    hw.close()
+    return out
+
+
 def _mean(xs):
     return sum(xs) / len(xs) if xs else S.NAN
 
@@ -179,6 +239,17 @@ def report(rows, meta, hw, gate_lines, mape_target, mape_ceiling):
     print("  mean regret@1 %.2f%% (ties broken pessimistically), worst %.2f%%" % (
         _mean([s.regret1[0] for s in ranking]) * 100, worst * 100))
     print("  largest group of equal predictions: %d configs\n" % max(s.largest_tie for s in ranking))
+    if rows and "schedule" in rows[0].record:
+        lo = launch_order_families(rows, hw)
+        print("launch order (rows that differ only in groupM): %d families" % lo.families)
+        print("  %d pairs with equal per-XCD footprints, all tied; measured difference median %.2f%%, max %.2f%%" % (
+            lo.equal_pairs, S.quantile(lo.equal_spread, 50) if lo.equal_spread else S.NAN,
+            max(lo.equal_spread) if lo.equal_spread else S.NAN))
+        print("  %d pairs with different footprints, ordered as measured: %d (%.0f%%)" % (
+            lo.ordered_pairs, lo.concordant, 100.0 * lo.concordant / lo.ordered_pairs if lo.ordered_pairs else 0))
+        print("  ties that do not follow the footprint: %d\n" % lo.violations)
+        if lo.violations:
+            failed.append("%d groupM pairs tie without equal footprints, or differ with them" % lo.violations)
     labels = collections.Counter(j.record["pred_bottleneck"] for j in rows)
     print("predicted bottleneck labels: %s" % ", ".join("%s %d" % kv for kv in labels.most_common()))
     print("counter cross-check: python -m ridge_amd.labelcheck\n")
