@@ -324,3 +324,38 @@ def test_concurrent_host_threads_launch_persistent_rows():
     assert not errors
     for (_, _, C, _) in jobs:
         assert np.array_equal(_bits(C), want)
+
+
+def test_launches_replay_from_a_captured_hip_graph():
+    """The launcher allocates nothing and never synchronises, so a caller can
+    capture kernel-table launches into a HIP graph and replay them (the way a
+    serving loop removes per-launch host cost). One row of each schedule is
+    captured on one stream; three replays, with the inputs refilled eagerly
+    between them, must each equal eager launches bit for bit."""
+    M, N, K = 1024, 1024, 1024
+    picks = []
+    for sched in (0, 1, 2):
+        cand = [v for v in G.variants() if v.schedule == sched and v.divides(M, N, K)]
+        assert cand, "no row of schedule %d divides %dx%dx%d" % (sched, M, N, K)
+        picks.append(cand[0])
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, 5)
+    G.fill_uniform(B, 6)
+    Cg = [torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV) for _ in picks]
+    for v in picks:  # eager first launches (the persistent launcher caches its grid)
+        _run(v.index, A, B, M, N, K)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for v, C in zip(picks, Cg):
+            assert G.launch(v.index, A, B, C, M, N, K) == 0
+    torch.cuda.synchronize()
+    for rep in range(3):
+        print("replay %d" % rep, flush=True)
+        G.fill_uniform(A, 100 + rep)
+        G.fill_uniform(B, 200 + rep)
+        graph.replay()
+        torch.cuda.synchronize()
+        for v, C in zip(picks, Cg):
+            eager = _run(v.index, A, B, M, N, K)
+            assert torch.equal(C, eager), "%s replay %d differs from the eager launch" % (v.label(), rep)
