@@ -142,6 +142,30 @@ def test_baseline_small_k_and_tall_skinny_exact_every_variant(M, N, K):
         assert bad == 0, "%s: %d of %d outputs differ" % (v.label(), bad, M * N)
 
 
+def _random_shapes(n, seed):
+    """Seeded shapes every row divides (M, N multiples of 256, K of 128) whose
+    grids are rarely a multiple of 8 or of the rows' GroupM: partial groups,
+    uneven XCD shares and single-tile-row grids."""
+    rng = np.random.default_rng(seed)
+    return [(256 * int(rng.integers(1, 6)), 256 * int(rng.integers(1, 6)), 128 * int(rng.integers(1, 9)))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,N,K", _random_shapes(6, 20261202))
+def test_random_divisible_shapes_exact_every_variant(M, N, K):
+    """Every row of the table on seeded odd-sized grids, small-integer inputs:
+    the FP16 output equals the exact product rounded once, and no output is
+    left unwritten (C starts as NaN)."""
+    Ab, Bb, want = _exact_case(M, N, K, -3, 3, M * 31 + N * 7 + K)
+    A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+    rows = [v for v in G.variants() if v.divides(M, N, K)]
+    assert len(rows) == G.num_variants()
+    for v in rows:
+        got = _bits(_run(v.index, A, B, M, N, K))
+        bad = int(np.count_nonzero(got != want))
+        assert bad == 0, "%s on %dx%dx%d: %d of %d outputs differ" % (v.label(), M, N, K, bad, M * N)
+
+
 def _persistent_edge_shapes(v):
     """Shapes that drive the persistent schedule's control flow to its edges."""
     BM, BN, BK, S = v.BM, v.BN, v.BK, v.stages
