@@ -1,0 +1,207 @@
+// probe_operand_stream.hip -- the operand loads of the tall-skinny GEMM, alone.
+//
+// The BASELINE tall-skinny shape (M = 16384, N = 128, K = 8192) runs on the
+// persistent 64x128x128 row: 256 workgroups, one per CU, each owning 64 rows of A
+// and all 128 columns, walking 64 K tiles of 128 from K tile (workgroup mod 64) and
+// wrapping. Per K tile a workgroup loads 16 KiB of A (64 rows x 256 bytes, from
+// HBM) and 32 KiB of B (128 x 128, the whole B being 2 MiB and L2-resident). This
+// probe issues exactly those loads, or parts of them, with no MFMAs and no C, so
+// the GEMM's time can be set against the time of its operand stream:
+//   A+B to LDS       the kernel's loads: A and B direct to an LDS ring of 3 stages,
+//                    two K tiles in flight, from two loader wavefronts
+//   A to LDS         the A loads alone, same ring and wavefronts
+//   A to LDS, in order   the same without the staggered K start
+//   A to VGPRs       four wavefronts each load their 16 rows of A into registers in
+//                    the MFMA fragment layout (16 rows x 64 bytes per instruction),
+//                    two K tiles in flight
+//   A to VGPRs + B to LDS   the same plus a quarter of each B tile per wavefront
+//                    direct to an LDS ring of 3 stages
+// Reported: TB/s of A (256 MiB per launch), warm (one operand set) and cold
+// (launches rotate over 3 sets, 768 MiB, beyond the 256 MB MALL), each the middle
+// of 5 windows of 30 launches after the warm-up. A diagnostic, not a calibration
+// constant: the model reads none of it.
+#include "cal_common.hpp"
+#include "gemm_mfma.hpp"
+
+using namespace ridgecal;
+
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int M = 16384, N = 128, K = 8192, BM = 64, BK = 128, NK = K / BK;
+constexpr int kTileA = BM * BK * 2;   // 16 KiB
+constexpr int kTileB = BK * N * 2;    // 32 KiB
+constexpr int kStages = 3;
+
+// Byte offset of lane `lane`'s 16-byte chunk in 1 KiB wave load `j` of a tile
+// whose rows are `rowBytes` apart in memory and `chunksPerRow` chunks wide.
+__device__ __forceinline__ uint32_t tileOffset(int j, int lane, int chunksPerRow, int rowBytes) {
+    const int q = j * 64 + lane;
+    return (uint32_t)((q / chunksPerRow) * rowBytes + (q % chunksPerRow) * 16);
+}
+
+// Two loader wavefronts stream A (and B when WITH_B) tiles into the ring: each
+// issues half of a tile's 1 KiB wave loads, waits until only the next tile's are
+// outstanding, then refills the stage of the tile before.
+template <bool WITH_B, bool STAGGER>
+__global__ __launch_bounds__(128) void loadsToLds(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                                                  unsigned* sink) {
+    __shared__ __attribute__((aligned(1024))) char lds[kStages * (kTileA + kTileB)];
+    constexpr int kLoadsA = kTileA / 1024 / 2, kLoadsB = WITH_B ? kTileB / 1024 / 2 : 0;
+    constexpr int kPerTile = kLoadsA + kLoadsB;
+    const int lane = threadIdx.x % 64;
+    const int l = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t base = ridge::ldsAddress(lds);
+    const char* panel = reinterpret_cast<const char*>(A + (size_t)blockIdx.x * BM * K);
+    uint32_t offA[kLoadsA], offB[kLoadsB > 0 ? kLoadsB : 1];
+#pragma unroll
+    for (int i = 0; i < kLoadsA; ++i) offA[i] = tileOffset(i * 2 + l, lane, BK / 8, K * 2);
+#pragma unroll
+    for (int i = 0; i < kLoadsB; ++i) offB[i] = tileOffset(i * 2 + l, lane, N / 8, N * 2);
+    const int start = STAGGER ? int(blockIdx.x % NK) : 0;
+    auto issue = [&](int g, int stage) {
+        const int k = (start + g) % NK;
+        const char* ta = panel + (size_t)k * BK * 2;
+#pragma unroll
+        for (int i = 0; i < kLoadsA; ++i) ridge::globalLoadLds16(ta, offA[i], base + stage * kTileA + (i * 2 + l) * 1024);
+        if constexpr (WITH_B) {
+            const char* tb = reinterpret_cast<const char*>(B) + (size_t)k * BK * N * 2;
+#pragma unroll
+            for (int i = 0; i < kLoadsB; ++i)
+                ridge::globalLoadLds16(tb, offB[i], base + kStages * kTileA + stage * kTileB + (i * 2 + l) * 1024);
+        }
+    };
+    issue(0, 0);
+    issue(1, 1);
+    for (int g = 0; g < NK; ++g) {
+        if (g + 1 < NK) {
+            ridge::waitVmcnt<kPerTile>();
+        } else {
+            ridge::waitVmcnt<0>();
+        }
+        if (g + 2 < NK) issue(g + 2, (g + 2) % kStages);
+    }
+    if (lane < 0) sink[0] = lds[lane];
+}
+
+// Four wavefronts, each loading its 16 rows of A into registers in the MFMA A
+// fragment layout (lane l: row l % 16, 16 bytes at k = 8 (l / 16) of each 32-deep
+// k-step), two K tiles in flight; with WITH_B each also loads a quarter of every B
+// tile direct to LDS. The A loads are inline asm so that the wait counts below,
+// which also cover the direct-to-LDS loads, are the only ones.
+template <bool WITH_B>
+__global__ __launch_bounds__(256) void loadsToVgpr(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                                                   unsigned* sink) {
+    __shared__ __attribute__((aligned(1024))) char lds[kStages * kTileB];
+    constexpr int kLoadsB = WITH_B ? kTileB / 1024 / 4 : 0;
+    constexpr int kPerTile = 4 + kLoadsB;
+    const int lane = threadIdx.x % 64;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t base = ridge::ldsAddress(lds);
+    const char* row = reinterpret_cast<const char*>(A + (size_t)(blockIdx.x * BM + w * 16 + lane % 16) * K) +
+                      16 * (lane / 16);
+    uint32_t offB[kLoadsB > 0 ? kLoadsB : 1];
+#pragma unroll
+    for (int i = 0; i < kLoadsB; ++i) offB[i] = tileOffset(i * 4 + w, lane, N / 8, N * 2);
+    const int start = int(blockIdx.x % NK);
+    u32x4 buf[2][4];
+    unsigned acc = 0;
+    auto issue = [&](int g, u32x4 (&b)[4]) {
+        const int k = (start + g) % NK;
+        const char* p = row + (size_t)k * BK * 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(b[j]) : "v"(p + 64 * j) : "memory");
+        if constexpr (WITH_B) {
+            const char* tb = reinterpret_cast<const char*>(B) + (size_t)k * BK * N * 2;
+#pragma unroll
+            for (int i = 0; i < kLoadsB; ++i)
+                ridge::globalLoadLds16(tb, offB[i], base + (g % kStages) * kTileB + (i * 4 + w) * 1024);
+        }
+    };
+    issue(0, buf[0]);
+    issue(1, buf[1]);
+    for (int g = 0; g < NK; g += 2) {
+        ridge::waitVmcnt<kPerTile>();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc ^= buf[0][j][0] ^ buf[0][j][3];
+        if (g + 2 < NK) issue(g + 2, buf[0]);
+        if (g + 2 < NK) {
+            ridge::waitVmcnt<kPerTile>();
+        } else {
+            ridge::waitVmcnt<0>();
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc ^= buf[1][j][0] ^ buf[1][j][3];
+        if (g + 3 < NK) issue(g + 3, buf[1]);
+    }
+    ridge::waitVmcnt<0>();
+    if (acc == 0x9e3779b9u) sink[0] = acc + (unsigned)lds[lane];
+}
+
+// The middle of 5 windows of `launches` launches, launch i reading set i % n, in
+// seconds per launch.
+template <typename Launch>
+double timeLaunches(Launch launch, int n, int launches) {
+    for (int i = 0; i < 3 * launches; ++i) launch(i % n);
+    CAL_HIP_CHECK(hipGetLastError());
+    CAL_HIP_CHECK(hipDeviceSynchronize());
+    hipEvent_t e0, e1;
+    CAL_HIP_CHECK(hipEventCreate(&e0));
+    CAL_HIP_CHECK(hipEventCreate(&e1));
+    std::vector<double> sec;
+    for (int w = 0; w < 5; ++w) {
+        CAL_HIP_CHECK(hipEventRecord(e0, nullptr));
+        for (int i = 0; i < launches; ++i) launch(i % n);
+        CAL_HIP_CHECK(hipEventRecord(e1, nullptr));
+        CAL_HIP_CHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        CAL_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        sec.push_back(ms * 1e-3 / launches);
+    }
+    CAL_HIP_CHECK(hipEventDestroy(e0));
+    CAL_HIP_CHECK(hipEventDestroy(e1));
+    return middle(sec);
+}
+
+}  // namespace
+
+int main() {
+    deviceBanner();
+    warmUp();
+    const size_t bytesA = (size_t)M * K * 2, bytesB = (size_t)K * N * 2;
+    constexpr int kSets = 3;
+    std::vector<_Float16*> As(kSets), Bs(kSets);
+    for (int s = 0; s < kSets; ++s) {
+        CAL_HIP_CHECK(hipMalloc(&As[s], bytesA));
+        CAL_HIP_CHECK(hipMalloc(&Bs[s], bytesB));
+        CAL_HIP_CHECK(hipMemset(As[s], 0x3c, bytesA));
+        CAL_HIP_CHECK(hipMemset(Bs[s], 0x3c, bytesB));
+    }
+    unsigned* sink = nullptr;
+    CAL_HIP_CHECK(hipMalloc(&sink, sizeof(unsigned)));
+    std::printf("\noperand loads of the 16384 x 128 x 8192 GEMM's 64x128x128 persistent row, no compute\n");
+    auto report = [&](const char* name, const char* key, auto kern, int threads) {
+        double t[2];
+        for (int cold = 0; cold < 2; ++cold) {
+            t[cold] = timeLaunches([&](int s) {
+                const int set = cold ? s : 0;
+                hipLaunchKernelGGL(kern, dim3(M / BM), dim3(threads), 0, nullptr, As[set], Bs[set], sink);
+            }, cold ? kSets : 1, 30);
+        }
+        std::printf("  %-26s warm %6.2f TB/s of A (%6.1f us)   cold %6.2f TB/s of A (%6.1f us)\n", name,
+                    bytesA / t[0] / 1e12, t[0] * 1e6, bytesA / t[1] / 1e12, t[1] * 1e6);
+        std::printf("PROBE operandStream %s warmSeconds %.6e coldSeconds %.6e aBytes %zu\n", key, t[0], t[1], bytesA);
+    };
+    report("A+B to LDS (the kernel's)", "ldsAB", loadsToLds<true, true>, 128);
+    report("A to LDS", "ldsA", loadsToLds<false, true>, 128);
+    report("A to LDS, K in order", "ldsAInOrder", loadsToLds<false, false>, 128);
+    report("A to VGPRs", "vgprA", loadsToVgpr<false>, 256);
+    report("A to VGPRs + B to LDS", "vgprAldsB", loadsToVgpr<true>, 256);
+    for (int s = 0; s < kSets; ++s) {
+        CAL_HIP_CHECK(hipFree(As[s]));
+        CAL_HIP_CHECK(hipFree(Bs[s]));
+    }
+    CAL_HIP_CHECK(hipFree(sink));
+    return 0;
+}
