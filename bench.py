@@ -70,6 +70,8 @@ HELDOUT_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout.csv")
 HELDOUT_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout-hw.json")
 HELDOUT2_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout2.csv")
 HELDOUT2_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout2-hw.json")
+HELDOUT3_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout3.csv")
+HELDOUT3_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout3-hw.json")
 # Host threads for the CPU baseline: the cores this process may use, capped at
 # the 16 a GPU box grants one GPU.
 MAX_CPU_THREADS = 16
@@ -254,9 +256,9 @@ def measured_traffic(M, N, K, key):
 def autotune_regret(k=10):
     """The pruner's regret at top-1 and top-k with the random-shortlist baseline,
     on the committed in-sample sweep (data/measured/mi355x.csv, 14 shapes x 24
-    variants, current calibration) and on the two held-out sweeps, each
+    variants, current calibration) and on the three held-out sweeps, each
     registered before it was measured and scored with the constants frozen with
-    it (data/measured/mi355x-heldout.csv, mi355x-heldout2.csv); a property of the
+    it (data/measured/mi355x-heldout.csv, mi355x-heldout2.csv, mi355x-heldout3.csv); a property of the
     sweeps and the model, not of this run's timing. None of it is computed if
     the model CLI is not built."""
     try:
@@ -264,7 +266,8 @@ def autotune_regret(k=10):
         out = {"top_k": k, "source": "data/measured/mi355x.csv"}
         for name, measured, hw in (("in_sample", MEASURED_SWEEP, HARDWARE_JSON),
                                    ("held_out", HELDOUT_SWEEP, HELDOUT_HARDWARE_JSON),
-                                   ("held_out_2", HELDOUT2_SWEEP, HELDOUT2_HARDWARE_JSON)):
+                                   ("held_out_2", HELDOUT2_SWEEP, HELDOUT2_HARDWARE_JSON),
+                                   ("held_out_3", HELDOUT3_SWEEP, HELDOUT3_HARDWARE_JSON)):
             table, total, shapes, _ = AT.evaluate(measured, hw, ks=(1, k))
             base = AT.baselines(measured, hw, ks=(1, k))
             by_k = {r["k"]: r for r in table}

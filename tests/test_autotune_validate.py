@@ -240,7 +240,7 @@ def test_launch_order_footprints_hand_case():
 
 @pytest.mark.parametrize("name,concordant,ordered,equal", [
     ("mi355x", 63, 82, 58), ("mi355x-replicate", 62, 82, 58),
-    ("mi355x-heldout", 78, 87, 53), ("mi355x-heldout2", 59, 82, 58)])
+    ("mi355x-heldout", 78, 87, 53), ("mi355x-heldout2", 59, 82, 58), ("mi355x-heldout3", 82, 95, 45)])
 def test_groupm_predictions_tie_exactly_at_equal_footprints(name, concordant, ordered, equal):
     """On every committed measurement, rows that differ only in groupM get equal
     predictions exactly when their per-XCD footprints are equal; the measured

@@ -92,3 +92,48 @@ def test_second_heldout_figures_as_reported():
     base = AT.baselines(MEASURED2, FROZEN2, ks=(1, 10))
     assert base[1]["random"][0] == pytest.approx(24.46, abs=0.01)
     assert all(by_k[1]["mean_regret"] < v[0] for v in base[1].values())
+
+
+# The third held-out sweep (data/sweep/mi355x-heldout3.md): the same frozen model as
+# the second, new shapes (BASELINE configs excluded too), the current kernels.
+MEASURED3 = os.path.join(ROOT, "data", "measured", "mi355x-heldout3.csv")
+REGISTERED3 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout3-registered.csv")
+FROZEN3 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout3-hw.json")
+TABLE3 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout3-table.csv")
+BASELINE_SHAPES = os.path.join(ROOT, "data", "sweep", "mi355x-baseline-configs.csv")
+
+
+def test_third_heldout_shapes_are_new_and_fully_measured():
+    held = {s[:3] for s in T.read_shapes(REGISTERED3)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    assert len(held) == 14 and not held & earlier
+    frozen = T.read(TABLE3, require=V.KEY_COLUMNS)
+    keys = [tuple(frozen.number(i, c, int) for c in V.KEY_COLUMNS) for i in range(len(frozen))]
+    assert len(set(keys)) == 24
+    table = T.read(MEASURED3)
+    absent, unexpected = V.registered_gate(table.records, T.read_shapes(REGISTERED3), keys)
+    assert not absent and not unexpected
+    assert float(table.meta["canary_drift_fraction"]) <= 0.05
+    with open(FROZEN2) as a, open(FROZEN3) as b:
+        assert a.read() == b.read()
+
+
+def test_third_heldout_figures_as_reported():
+    """Every registered target met: regret at k = 1 below 10% on every shape (worst
+    4.15%) with a mean of 0.50%, and k = 10 finds every shape's best."""
+    rows = V.join(MEASURED3, FROZEN3)
+    assert sum(j.abs_pct for j in rows) / len(rows) == pytest.approx(10.10, abs=0.01)
+    ranking = V.rank_shapes(rows)
+    assert sum(s.rho for s in ranking) / len(ranking) == pytest.approx(0.863, abs=0.001)
+    table, total, shapes, _ = AT.evaluate(MEASURED3, FROZEN3, ks=(1, 10))
+    by_k = {r["k"]: r for r in table}
+    assert (total, shapes) == (336, 14)
+    assert by_k[1]["mean_regret"] == pytest.approx(0.50, abs=0.01) and by_k[1]["hits"] == 10
+    assert by_k[1]["max_regret"] == pytest.approx(4.15, abs=0.01)
+    assert by_k[10]["mean_regret"] == 0.0 and by_k[10]["hits"] == 14
+    base = AT.baselines(MEASURED3, FROZEN3, ks=(1, 10))
+    assert base[1]["random"][0] == pytest.approx(25.77, abs=0.01)
+    assert base[10]["random"][0] == pytest.approx(3.87, abs=0.01)
+    assert all(by_k[1]["mean_regret"] < v[0] for v in base[1].values())
