@@ -16,6 +16,10 @@
 //                    two K tiles in flight
 //   A to VGPRs + B to LDS   the same plus a quarter of each B tile per wavefront
 //                    direct to an LDS ring of 3 stages
+//   A+B, one tile in flight   the kernel's loads with a ring of 2 stages
+//   A+B, 128 rows, K split in 2   a split-K schedule's loads: workgroup w takes half
+//                    of the K range of a 128-row panel, so each B tile serves 128
+//                    rows instead of 64 (ring of 2 stages, to fit 160 KiB)
 // Reported: TB/s of A (256 MiB per launch), warm (one operand set) and cold
 // (launches rotate over 3 sets, 768 MiB, beyond the 256 MB MALL), each the middle
 // of 5 windows of 30 launches after the warm-up. A diagnostic, not a calibration
@@ -44,43 +48,57 @@ __device__ __forceinline__ uint32_t tileOffset(int j, int lane, int chunksPerRow
 // Two loader wavefronts stream A (and B when WITH_B) tiles into the ring: each
 // issues half of a tile's 1 KiB wave loads, waits until only the next tile's are
 // outstanding, then refills the stage of the tile before.
-template <bool WITH_B, bool STAGGER>
+// ROWS rows of A per workgroup; with SPLIT > 1 the K range is split into SPLIT
+// parts, workgroup w taking part w % SPLIT of row panel w / SPLIT (the loads of a
+// split-K schedule, which reads each B tile once per SPLIT * ROWS rows instead of
+// once per ROWS rows).
+// RING stages hold RING - 1 K tiles in flight.
+template <bool WITH_B, bool STAGGER, int ROWS = BM, int SPLIT = 1, int RING = kStages>
 __global__ __launch_bounds__(128) void loadsToLds(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                   unsigned* sink) {
-    __shared__ __attribute__((aligned(1024))) char lds[kStages * (kTileA + kTileB)];
-    constexpr int kLoadsA = kTileA / 1024 / 2, kLoadsB = WITH_B ? kTileB / 1024 / 2 : 0;
+    constexpr int kTileRows = ROWS * BK * 2;
+    constexpr int kTiles = NK / SPLIT;
+    constexpr int kAhead = RING - 1;
+    __shared__ __attribute__((aligned(1024))) char lds[RING * (kTileRows + kTileB)];
+    constexpr int kLoadsA = kTileRows / 1024 / 2, kLoadsB = WITH_B ? kTileB / 1024 / 2 : 0;
     constexpr int kPerTile = kLoadsA + kLoadsB;
+    static_assert(kAhead * kPerTile < 64, "a loader's tiles in flight must fit vmcnt");
+    static_assert(RING * (kTileRows + kTileB) <= 163840, "the ring must fit 160 KiB of LDS");
     const int lane = threadIdx.x % 64;
     const int l = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t base = ridge::ldsAddress(lds);
-    const char* panel = reinterpret_cast<const char*>(A + (size_t)blockIdx.x * BM * K);
+    const int panelIdx = blockIdx.x / SPLIT;
+    const int part = blockIdx.x % SPLIT;
+    const char* panel = reinterpret_cast<const char*>(A + (size_t)panelIdx * ROWS * K);
     uint32_t offA[kLoadsA], offB[kLoadsB > 0 ? kLoadsB : 1];
 #pragma unroll
     for (int i = 0; i < kLoadsA; ++i) offA[i] = tileOffset(i * 2 + l, lane, BK / 8, K * 2);
 #pragma unroll
     for (int i = 0; i < kLoadsB; ++i) offB[i] = tileOffset(i * 2 + l, lane, N / 8, N * 2);
-    const int start = STAGGER ? int(blockIdx.x % NK) : 0;
+    const int start = STAGGER ? int(panelIdx % kTiles) : 0;
     auto issue = [&](int g, int stage) {
-        const int k = (start + g) % NK;
+        const int k = part * kTiles + (start + g) % kTiles;
         const char* ta = panel + (size_t)k * BK * 2;
 #pragma unroll
-        for (int i = 0; i < kLoadsA; ++i) ridge::globalLoadLds16(ta, offA[i], base + stage * kTileA + (i * 2 + l) * 1024);
+        for (int i = 0; i < kLoadsA; ++i)
+            ridge::globalLoadLds16(ta, offA[i], base + stage * kTileRows + (i * 2 + l) * 1024);
         if constexpr (WITH_B) {
             const char* tb = reinterpret_cast<const char*>(B) + (size_t)k * BK * N * 2;
 #pragma unroll
             for (int i = 0; i < kLoadsB; ++i)
-                ridge::globalLoadLds16(tb, offB[i], base + kStages * kTileA + stage * kTileB + (i * 2 + l) * 1024);
+                ridge::globalLoadLds16(tb, offB[i], base + RING * kTileRows + stage * kTileB + (i * 2 + l) * 1024);
         }
     };
-    issue(0, 0);
-    issue(1, 1);
-    for (int g = 0; g < NK; ++g) {
-        if (g + 1 < NK) {
-            ridge::waitVmcnt<kPerTile>();
+    for (int g = 0; g < kAhead; ++g) issue(g, g);
+    for (int g = 0; g < kTiles; ++g) {
+        // Tile g has landed once at most the kAhead - 1 tiles after it are
+        // outstanding; then tile g + kAhead takes the stage of tile g - 1.
+        if (g + kAhead - 1 < kTiles) {
+            ridge::waitVmcnt<(kAhead - 1) * kPerTile>();
         } else {
             ridge::waitVmcnt<0>();
         }
-        if (g + 2 < NK) issue(g + 2, (g + 2) % kStages);
+        if (g + kAhead < kTiles) issue(g + kAhead, (g + kAhead) % RING);
     }
     if (lane < 0) sink[0] = lds[lane];
 }
@@ -198,6 +216,8 @@ int main() {
     report("A to LDS, K in order", "ldsAInOrder", loadsToLds<false, false>, 128);
     report("A to VGPRs", "vgprA", loadsToVgpr<false>, 256);
     report("A to VGPRs + B to LDS", "vgprAldsB", loadsToVgpr<true>, 256);
+    report("A+B, one tile in flight", "ldsABring2", loadsToLds<true, true, BM, 1, 2>, 128);
+    report("A+B, 128 rows, K split in 2", "ldsABsplit2", loadsToLds<true, true, 128, 2, 2>, 128);
     for (int s = 0; s < kSets; ++s) {
         CAL_HIP_CHECK(hipFree(As[s]));
         CAL_HIP_CHECK(hipFree(Bs[s]));
