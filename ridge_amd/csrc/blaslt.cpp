@@ -46,8 +46,12 @@ int makeLayouts(Plan& p, int M, int N, int K, int cF32) {
     hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     if (st != HIPBLAS_STATUS_SUCCESS) return (int)st;
     const int32_t opN = HIPBLAS_OP_N;
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opN, sizeof(opN));
-    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN));
+    if ((st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opN, sizeof(opN))) !=
+        HIPBLAS_STATUS_SUCCESS)
+        return (int)st;
+    if ((st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN))) !=
+        HIPBLAS_STATUS_SUCCESS)
+        return (int)st;
     // Column-major view: first operand B^T is N x K (ld N), second A^T is K x M
     // (ld K), result C^T is N x M (ld N).
     if ((st = hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16F, N, K, N)) != HIPBLAS_STATUS_SUCCESS) return (int)st;

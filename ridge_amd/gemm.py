@@ -209,9 +209,13 @@ def _check_operands(A, B, C=None):
         raise RidgeGemmError("shapes %s x %s do not chain" % (tuple(A.shape), tuple(B.shape)))
     if not (A.is_contiguous() and B.is_contiguous()):
         raise RidgeGemmError("A and B must be row-major contiguous")
+    if A.device != B.device:
+        raise RidgeGemmError("A is on %s but B on %s" % (A.device, B.device))
     if C is not None:
         if C.dtype != torch.float16 or not C.is_contiguous() or tuple(C.shape) != (A.shape[0], B.shape[1]):
             raise RidgeGemmError("C must be a contiguous float16 tensor of shape (M, N)")
+        if C.device != A.device:
+            raise RidgeGemmError("C is on %s but A and B on %s" % (C.device, A.device))
 
 
 def gemm(A, B, index=0, out=None, stream=None):
@@ -221,7 +225,9 @@ def gemm(A, B, index=0, out=None, stream=None):
     M, K = A.shape
     N = B.shape[1]
     C = out if out is not None else torch.empty((M, N), dtype=torch.float16, device=A.device)
-    rc = launch(index, A, B, C, M, N, K, stream)
+    # The library launches on the current device; make it the operands' one.
+    with torch.cuda.device(A.device):
+        rc = launch(index, A, B, C, M, N, K, stream)
     if rc != HIP_SUCCESS:
         raise RidgeGemmError("ridge_gemm_launch(variant %d, %dx%dx%d) returned hipError %d" % (index, M, N, K, rc))
     return C

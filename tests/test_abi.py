@@ -89,6 +89,16 @@ def test_divisibility_and_bad_launches_are_rejected_before_any_gpu_call():
         G.variant(24)
 
 
+def test_gemm_refuses_bad_operands_before_any_launch():
+    import torch
+    a = torch.zeros((256, 64), dtype=torch.float16)
+    b = torch.zeros((64, 256), dtype=torch.float16)
+    with pytest.raises(G.RidgeGemmError, match="float16"):
+        G.gemm(a.float(), b)
+    with pytest.raises(G.RidgeGemmError, match="device tensors"):
+        G.gemm(a, b)
+
+
 def test_variant_table_csv():
     text = G.variant_table_csv()
     lines = text.strip().splitlines()
