@@ -69,12 +69,12 @@ void splitKKernel(const _Float16* __restrict__ A, const _Float16* __restrict__ B
 #pragma unroll
         for (int i = 0; i < P::kLoadsA; ++i) {
             const int q = ridge::swizzleA<T::kChunksPerRowA>((i * P::kLoaders + l) * 64 + lane);
-            offA[i] = (uint32_t)(((q / T::kChunksPerRowA) * K + (q % T::kChunksPerRowA) * 8) * 2);
+            offA[i] = ridge::tileOffset(q / T::kChunksPerRowA, K, q % T::kChunksPerRowA);
         }
 #pragma unroll
         for (int i = 0; i < P::kLoadsB; ++i) {
             const int q = ridge::swizzleB<T::kChunksPerRowB>((i * P::kLoaders + l) * 64 + lane);
-            offB[i] = (uint32_t)(((q / T::kChunksPerRowB) * N + (q % T::kChunksPerRowB) * 8) * 2);
+            offB[i] = ridge::tileOffset(q / T::kChunksPerRowB, N, q % T::kChunksPerRowB);
         }
         int row, col;
         ridge::tileOf<BM, BN, GROUPM>(tile, M, N, row, col);

@@ -159,6 +159,13 @@ __device__ __forceinline__ void globalLoadLds16(const void* base, uint32_t offse
 }
 
 // LDS byte address of a __shared__ object, as a wave-uniform scalar.
+// Byte offset of 16-byte chunk `chunk` of row `row` in an FP16 tile whose rows are
+// `ld` elements apart. Unsigned 32-bit arithmetic: the launcher admits only shapes
+// with BM * K and BK * N below 2^31, so every tile offset is below 2^32.
+__device__ __forceinline__ uint32_t tileOffset(int row, int ld, int chunk) {
+    return ((uint32_t)row * (uint32_t)ld + (uint32_t)chunk * 8u) * 2u;
+}
+
 __device__ __forceinline__ uint32_t ldsAddress(const void* p) {
     return __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const RIDGE_LDS_AS char*)(static_cast<const char*>(p)));
@@ -345,12 +352,12 @@ struct GemmBlock {
 #pragma unroll
         for (int i = 0; i < T::kPerWaveA; ++i) {
             const int q = swizzleA<CPR_A>((i * T::kWaves + wave) * 64 + lane);
-            offA[i] = (uint32_t)(((q / CPR_A) * K + (q % CPR_A) * 8) * 2);
+            offA[i] = tileOffset(q / CPR_A, K, q % CPR_A);
         }
 #pragma unroll
         for (int i = 0; i < T::kPerWaveB; ++i) {
             const int q = swizzleB<CPR_B>((i * T::kWaves + wave) * 64 + lane);
-            offB[i] = (uint32_t)(((q / CPR_B) * N + (q % CPR_B) * 8) * 2);
+            offB[i] = tileOffset(q / CPR_B, N, q % CPR_B);
         }
         // A fragment of tile tm, k-step ks: row waveM*WM + 16 tm + lane%16,
         // logical chunk 4 ks + lane/16 (k = 32 ks + 8 (lane/16) .. +7).
@@ -737,12 +744,12 @@ void gemmMfmaPersistentKernel(const _Float16* __restrict__ A, const _Float16* __
 #pragma unroll
         for (int i = 0; i < P::kLoadsA; ++i) {
             const int q = swizzleA<T::kChunksPerRowA>((i * P::kLoaders + l) * 64 + lane);
-            offA[i] = (uint32_t)(((q / T::kChunksPerRowA) * K + (q % T::kChunksPerRowA) * 8) * 2);
+            offA[i] = tileOffset(q / T::kChunksPerRowA, K, q % T::kChunksPerRowA);
         }
 #pragma unroll
         for (int i = 0; i < P::kLoadsB; ++i) {
             const int q = swizzleB<T::kChunksPerRowB>((i * P::kLoaders + l) * 64 + lane);
-            offB[i] = (uint32_t)(((q / T::kChunksPerRowB) * N + (q % T::kChunksPerRowB) * 8) * 2);
+            offB[i] = tileOffset(q / T::kChunksPerRowB, N, q % T::kChunksPerRowB);
         }
         // K tiles are issued in a fixed order, so a cursor (output tile, K
         // tile) replaces per-issue index arithmetic. An output tile's K loop

@@ -89,6 +89,18 @@ def test_divisibility_and_bad_launches_are_rejected_before_any_gpu_call():
         G.variant(24)
 
 
+def test_offset_guard_admits_up_to_2_pow_31_and_refuses_beyond():
+    """In-kernel byte offsets into an A or B tile are 32-bit: a shape is admitted
+    only while BM * K and BK * N stay below 2^31."""
+    for v in G.variants():
+        k_max = (0x7FFFFFFF // v.BM) // v.BK * v.BK
+        assert v.divides(v.BM, v.BN, k_max), v.label()
+        assert not v.divides(v.BM, v.BN, k_max + v.BK), v.label()
+        n_max = (0x7FFFFFFF // v.BK) // v.BN * v.BN
+        assert v.divides(v.BM, n_max, v.BK), v.label()
+        assert not v.divides(v.BM, n_max + v.BN, v.BK), v.label()
+
+
 def test_gemm_refuses_bad_operands_before_any_launch():
     import torch
     a = torch.zeros((256, 64), dtype=torch.float16)

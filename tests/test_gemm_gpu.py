@@ -197,6 +197,48 @@ def test_persistent_rows_edge_shapes_bit_exact():
             assert bad == 0, "%s on %dx%dx%d: %d of %d outputs differ" % (v.label(), M, N, K, bad, M * N)
 
 
+# The launcher admits a shape only while its 32-bit in-kernel byte offsets cannot
+# overflow (BM * K and BK * N below 2^31). At the largest K it admits for 256-row
+# tiles, an A tile's last row starts (BM - 1) * K * 2 bytes, just under 2^32, into
+# the tile's row panel.
+K_LIMIT_BM256 = (0x7FFFFFFF // 256) // 64 * 64
+
+
+def _offset_limit_case(M, N, K):
+    """A[i, k] = 1 where k = i (mod 4099) and B[k, j] = 1 where k = j (mod 3), else
+    0. C[i, j] counts the k < K in both classes: with k = i + 4099 t and
+    4099 = 1 (mod 3), those are the t < T_i = ceil((K - i) / 4099) with
+    t = j - i (mod 3). Every count is near 682, exact in FP16, and a wrapped
+    offset reads another row's or another K slice's classes."""
+    k = torch.arange(K, device=DEV, dtype=torch.int32)
+    A = (k[None, :] % 4099 == torch.arange(M, device=DEV, dtype=torch.int32)[:, None]).to(torch.float16)
+    rows = (torch.arange(3, device=DEV)[:, None] - torch.arange(N, device=DEV)[None, :]) % 3 == 0
+    B = rows.to(torch.float16).index_select(0, (k % 3).long())
+    del k
+    i = np.arange(M)[:, None]
+    j = np.arange(N)[None, :]
+    T = (K - i + 4098) // 4099
+    r = (j - i) % 3
+    count = np.where(r < T, (T - r + 2) // 3, 0)
+    return A, B, count.astype(np.float16).view(np.uint16).ravel()
+
+
+def test_largest_k_the_offset_guard_admits_is_exact():
+    M = N = 256
+    K = K_LIMIT_BM256
+    rows = [v for v in G.variants() if v.BM == 256 and v.divides(M, N, K)]
+    assert rows, "no 256-row variant admits the limit shape"
+    print("  K = %d, %d variants" % (K, len(rows)), flush=True)
+    A, B, want = _offset_limit_case(M, N, K)
+    for v in rows:
+        print("  variant %d %s" % (v.index, v.label()), flush=True)
+        got = _bits(_run(v.index, A, B, M, N, K))
+        bad = int(np.count_nonzero(got != want))
+        assert bad == 0, "%s at K = %d: %d of %d outputs differ" % (v.label(), K, bad, M * N)
+    del A, B
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 128),
                                    (16384, 128, 8192)])
 def test_baseline_configs_uniform_inputs(M, N, K):
