@@ -68,8 +68,9 @@ int ridge_gemm_get_variant(int i, ridge_gemm_variant_t* out);
 int ridge_gemm_find_variant(int BM, int BN, int BK, int WM, int WN, int stages, int groupM);
 
 /* 1 when variant i can run M x N x K (M%BM == N%BN == K%BK == 0, K >= BK, all
- * positive), else 0. The reference leaves this check to its callers
- * (check-gemm.cu:303, measure.cu:244). */
+ * positive, and BM*K, BK*N and the tile count below 2^31, which keeps the
+ * kernels' 32-bit tile offsets exact), else 0. The reference leaves this check
+ * to its callers (check-gemm.cu:303, measure.cu:244). */
 int ridge_gemm_divides(int i, int M, int N, int K);
 
 /* C = A * B with variant i. A: M x K, B: K x N, C: M x N, all row-major FP16 in
