@@ -42,9 +42,10 @@ autotune: the metric's second half, the mean top-10 regret of the model-pruned
 autotuner, is computed from the committed measured sweep (data/measured/mi355x.csv,
 14 shapes x 24 variants) and the committed calibration (data/hardware/mi355x.json)
 by ridge_amd.autotune, with regret at top-1 and the expected regret of a random
-shortlist beside it, and the same for the held-out sweep registered before it was
-measured (data/measured/mi355x-heldout.csv, frozen constants); it is a property of
-the sweeps and the model, not of this run's timing.
+shortlist beside it, and the same for the three held-out sweeps, each registered
+before it was measured and scored with the constants frozen beside it
+(data/measured/mi355x-heldout*.csv); it is a property of the sweeps and the model,
+not of this run's timing.
 """
 
 import argparse
