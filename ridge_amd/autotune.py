@@ -46,10 +46,10 @@ def load_rows(path):
     return T.read(path).records
 
 
-def predicted_rows(measured, hw):
+def predicted_rows(measured, hw, binary=None):
     with tempfile.TemporaryDirectory() as tmp:
         out = os.path.join(tmp, "pred.csv")
-        RM.predict_batch(measured, out, hw=hw)
+        RM.predict_batch(measured, out, hw=hw, binary=binary or RM.PREDICT_BIN)
         return T.read(out, require=("pred_tflops",)).records
 
 
@@ -83,9 +83,9 @@ def random_regret_at_k(shapes, k):
     return statistics.mean(per), max(per)
 
 
-def evaluate(measured, hw, ks=DEFAULT_KS):
+def evaluate(measured, hw, ks=DEFAULT_KS, binary=None):
     meas = load_rows(measured)
-    pred = predicted_rows(measured, hw)
+    pred = predicted_rows(measured, hw, binary)
     shapes = group_by_shape(meas, pred)
     per_shape = len(meas) // len(shapes)
     table = []
@@ -99,11 +99,11 @@ def evaluate(measured, hw, ks=DEFAULT_KS):
     return table, len(meas), len(shapes), per_shape
 
 
-def baselines(measured, hw, ks=DEFAULT_KS):
+def baselines(measured, hw, ks=DEFAULT_KS, binary=None):
     """{k: {name: (mean regret %, max regret %)}} for the random shortlist and
     the model-free rankings."""
     meas = load_rows(measured)
-    pred = predicted_rows(measured, hw)
+    pred = predicted_rows(measured, hw, binary)
     by_heuristic = {name: group_by_shape(meas, pred, f) for name, f in HEURISTICS.items()}
     shapes = group_by_shape(meas, pred)
     per_shape = min(len(v) for v in shapes.values())
@@ -123,7 +123,9 @@ def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--measured", default=os.path.join(ROOT, "data", "measured", "mi355x.csv"))
     ap.add_argument("--hw", default=os.path.join(ROOT, "data", "hardware", "mi355x.json"))
-    ap.add_argument("--k", default=",".join(str(k) for k in DEFAULT_KS))
+    ap.add_argument("--predict-bin", default=RM.PREDICT_BIN, help="the ridge-predict executable")
+    ap.add_argument("--k", default=",".join(str(k) for k in DEFAULT_KS),
+                    help="shortlist sizes to evaluate, per shape")
     ap.add_argument("--target-k", type=int, default=10)
     ap.add_argument("--target-regret", type=float, default=2.0)
     args = ap.parse_args(argv)
@@ -132,9 +134,9 @@ def main(argv=None):
     hw = args.hw if (args.hw in ("a100", "mi355x") or os.path.exists(args.hw)) else "mi355x"
     ks = [int(x) for x in args.k.split(",")]
     try:
-        table, total, nshapes, per_shape = evaluate(args.measured, hw, ks)
-        base = baselines(args.measured, hw, ks)
-    except T.TableError as e:
+        table, total, nshapes, per_shape = evaluate(args.measured, hw, ks, args.predict_bin)
+        base = baselines(args.measured, hw, ks, args.predict_bin)
+    except (T.TableError, RuntimeError) as e:
         sys.exit(str(e))
 
     print("Model-pruned empirical autotuner")

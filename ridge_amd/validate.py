@@ -64,10 +64,10 @@ class Joined:
         return abs(self.signed_pct)
 
 
-def join(measured_path, hw):
+def join(measured_path, hw, binary=None):
     with tempfile.TemporaryDirectory() as td:
         out = os.path.join(td, "pred.csv")
-        sys.stderr.write(RM.predict_batch(measured_path, out, hw=hw))
+        sys.stderr.write(RM.predict_batch(measured_path, out, hw=hw, binary=binary or RM.PREDICT_BIN))
         table = T.read(out, require=("M", "N", "K", "tflops", "pred_tflops", "pred_bottleneck") + KEY_COLUMNS)
     return [Joined(r, table.number(i, "tflops"), table.number(i, "pred_tflops")) for i, r in enumerate(table)]
 
@@ -263,6 +263,7 @@ def main(argv=None):
     ap.add_argument("--measured", default=os.path.join(ROOT, "data", "measured", "mi355x.csv"))
     ap.add_argument("--registered", default=os.path.join(ROOT, "data", "sweep", "mi355x-registered.csv"))
     ap.add_argument("--hw", default=os.path.join(ROOT, "data", "hardware", "mi355x.json"))
+    ap.add_argument("--predict-bin", default=RM.PREDICT_BIN, help="the ridge-predict executable")
     ap.add_argument("--max-mape", type=float, default=10.0)
     ap.add_argument("--fail-mape", type=float, default=15.0)
     ap.add_argument("--no-table-gate", action="store_true",
@@ -270,7 +271,7 @@ def main(argv=None):
     args = ap.parse_args(argv)
     try:
         meta = T.read(args.measured).meta
-        rows = join(args.measured, args.hw)
+        rows = join(args.measured, args.hw, args.predict_bin)
         if not rows:
             raise T.TableError(args.measured, 0, "no measured rows")
         gate_lines, failed = [], []
@@ -288,7 +289,7 @@ def main(argv=None):
             else:
                 gate_lines.append("  the measured rows are exactly the registered cross product")
             gate_lines.append("")
-    except T.TableError as e:
+    except (T.TableError, RuntimeError) as e:
         sys.exit(str(e))
     failed += report(rows, meta, args.hw, gate_lines, args.max_mape, args.fail_mape)
     for f in failed:

@@ -159,6 +159,17 @@ def test_autotune_end_to_end_on_reference_a100_sweep():
     assert 0.0 < k1["mean_regret"] < 15.0
 
 
+def test_predict_bin_flag_is_honoured_by_both_tools():
+    """The reference's tools take --predict-bin (ridge-autotune.py:45,
+    validate.py:193); a missing executable ends the run with the path named."""
+    for main in (AT.main, V.main):
+        with pytest.raises(SystemExit) as e:
+            main(["--predict-bin", "/nonexistent/ridge-predict"])
+        assert "/nonexistent/ridge-predict" in str(e.value)
+    from ridge_amd import model as RM
+    assert AT.main(["--predict-bin", RM.PREDICT_BIN, "--k", "1,10"]) == 0
+
+
 def test_measured_mi355x_sweep_is_the_registered_cross_product():
     """The committed MI355X sweep covers exactly shapes x table (the measurement
     integrity gate of bench/validate.py:136-156)."""
