@@ -111,6 +111,16 @@ def test_gemm_refuses_bad_operands_before_any_launch():
         G.gemm(a, b)
 
 
+def test_ridge_check_lists_the_variant_table_without_a_gpu():
+    import subprocess
+    exe = os.path.join(ROOT, "ridge_amd", "bin", "ridge-check")
+    out = subprocess.run([exe, "--list-variants"], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout == G.variant_table_csv()
+    bad = subprocess.run([exe, "--no-such-option"], capture_output=True, text=True, timeout=60)
+    assert bad.returncode == 2 and "unknown option" in bad.stderr
+
+
 def test_variant_table_csv():
     text = G.variant_table_csv()
     lines = text.strip().splitlines()
