@@ -172,6 +172,37 @@ def test_random_divisible_shapes_exact_every_variant(M, N, K):
         assert bad == 0, "%s on %dx%dx%d: %d of %d outputs differ" % (v.label(), M, N, K, bad, M * N)
 
 
+# Random-data twin of the test above: 3 shapes by default, RIDGE_RANDOM_UNIFORM_SHAPES=n
+# draws n (another seed).
+RANDOM_UNIFORM_SHAPES = int(os.environ.get("RIDGE_RANDOM_UNIFORM_SHAPES", "3"))
+
+
+@pytest.mark.parametrize("M,N,K", _random_shapes(RANDOM_UNIFORM_SHAPES, 20261203))
+def test_random_divisible_shapes_uniform_inputs_every_variant(M, N, K):
+    """Every row of the table on seeded odd-sized grids with U[-1,1) inputs,
+    against the f64 oracle under the reference's gates and the FP16-output gate
+    (every element within FP32 accumulation plus one rounding). All rows of C up
+    to 2^30 multiply-adds, 128 evenly spaced rows beyond."""
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, M * 131 + N * 17 + K)
+    G.fill_uniform(B, M * 7 + N * 131 + K + 1)
+    Ab, Bb = _bits(A), _bits(B)
+    rows = np.arange(M) if M * N * K <= 2 ** 30 else np.linspace(0, M - 1, 128).astype(int)
+    Arows = Ab.reshape(M, K)[rows].ravel()
+    ref = O.gemm_f64(Arows, Bb, len(rows), N, K)
+    absprod = O.gemm_f64(O.abs_bits(Arows), O.abs_bits(Bb), len(rows), N, K)
+    max_a, max_b = _max_abs(Ab), _max_abs(Bb)
+    for v in G.variants():
+        assert v.divides(M, N, K)
+        got = O.f16_bits_to_f32(_bits(_run(v.index, A, B, M, N, K))).reshape(M, N)[rows]
+        ok, frob, mx, ne = O.passes(got, ref, max_a, max_b, K)
+        assert ok, "%s on %dx%dx%d: frob %.3e maxRel %.3e norm %.3e" % (v.label(), M, N, K, frob, mx, ne)
+        ok, frob, worst = O.passes_fp16(got, ref, absprod, K)
+        assert ok, "%s on %dx%dx%d: FP16-output gate frob %.3e, worst element at %.2f of its bound" % (
+            v.label(), M, N, K, frob, worst)
+
+
 def _persistent_edge_shapes(v):
     """Shapes that drive the persistent schedule's control flow to its edges."""
     BM, BN, BK, S = v.BM, v.BN, v.BK, v.stages
