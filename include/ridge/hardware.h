@@ -109,6 +109,12 @@ struct HardwareModel {
                                      //    skeleton's row (128x128x64 w64x64 s4 with one compute wave
                                      //    per SIMD, 256x128x32 w64x64 s6 with two)
     double persistentStepCycles[2] = {0.0, 0.0};  // [CAL] cycles per K tile of those two skeletons
+    int mallReuseModel = 0;          // 0: every A/B byte an XCD's L2 misses is read from HBM (reference:
+                                     //    one cache level)
+                                     // 1: when A and B fit in the MALL (mallBytes), HBM supplies each
+                                     //    once and the L2s' further misses (other XCDs re-fetching the
+                                     //    same panels) are MALL hits at mallRefillBytesPerSec, in series
+    double mallBytes = 0.0;          // capacity of the memory-side cache in front of HBM (datasheet)
     int fillShareModel = 0;          // 0: every workgroup fetches its first tiles from HBM (reference)
                                      // 1: the resident workgroups' first tiles come from HBM once per
                                      //    distinct panel an XCD holds (the kernels' launch order) and

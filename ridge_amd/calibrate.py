@@ -22,6 +22,8 @@ MI355X differences from the reference driver:
     1/2 .. 1/16 of the CUs busy (clockRatio*: the model's clockModel 1), the
     per-operand LDS rates feed ldsReadModel 1, and cal-hbm-bw's L2-resident read
     (l2HitBytesPerCycle) feeds l2StreamModel 1;
+  * the MALL's capacity (datasheet) with the calibrated refill rate feeds
+    mallReuseModel 1: when A and B fit, re-fetches of their panels are MALL hits;
   * cal-smem-bw's ping-pong skeleton figures (reads under MFMAs, with and without
     the GEMM's direct-to-LDS refill) are kept in the JSON as a record, and the ratio
     of its clock with the refill to its clock with MFMAs alone is loadedClockRatio
@@ -41,7 +43,8 @@ ROOT = os.path.dirname(PKG)
 
 # Public datasheet figures, cross-checks only.
 SPECS = {
-    "gfx950": dict(name="MI355X", peak_tflops=2516.6, hbm_bytes_per_sec=8.0e12, cus=256, clock_hz=2.4e9),
+    "gfx950": dict(name="MI355X", peak_tflops=2516.6, hbm_bytes_per_sec=8.0e12, cus=256, clock_hz=2.4e9,
+                   mall_bytes=256 << 20),
 }
 
 BENCHMARKS = ["cal-mma", "cal-smem-bw", "cal-hbm-bw", "cal-latency"]
@@ -218,6 +221,11 @@ def hardware_json(res, spec, arch):
                 ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
         if key in res:
             out[key] = res[key]
+    if "mallRefillBytesPerSec" in res:
+        # The MALL's capacity is a datasheet figure; the rate its hits move at
+        # is the calibrated refill path's.
+        out["mallBytes"] = spec["mall_bytes"]
+        out["mallReuseModel"] = 1
     for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]), ("fillLatencyModel", ["fillLatencySec"]),
                         ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)]),
                         ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"])):

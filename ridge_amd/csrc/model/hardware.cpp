@@ -120,7 +120,7 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("mallStretch1", h.mallStretch[1]), R("mallStretch2", h.mallStretch[2]), R("mallStretch3", h.mallStretch[3]),
         R("mallStretch4", h.mallStretch[4]), I("persistentStepModel", h.persistentStepModel),
         R("persistentStepCycles1", h.persistentStepCycles[0]), R("persistentStepCycles2", h.persistentStepCycles[1]),
-        I("fillShareModel", h.fillShareModel),
+        I("fillShareModel", h.fillShareModel), I("mallReuseModel", h.mallReuseModel), R("mallBytes", h.mallBytes),
     };
 }
 
@@ -181,6 +181,8 @@ std::string inconsistency(const HardwareModel& h) {
         return "fillLatencyModel 1 reads fillLatencySec, which must be positive";
     if (h.fillShareModel == 1 && !(h.l2HitBytesPerCycle > 0.0))
         return "fillShareModel 1 reads l2HitBytesPerCycle, which must be positive";
+    if (h.mallReuseModel == 1 && !(h.mallRefillBytesPerSec > 0.0 && h.mallBytes > 0.0))
+        return "mallReuseModel 1 reads mallRefillBytesPerSec and mallBytes, which must be positive";
     if (h.persistentStepModel == 1 && !(h.persistentStepCycles[0] > 0.0 && h.persistentStepCycles[1] > 0.0))
         return "persistentStepModel 1 reads persistentStepCycles1 and persistentStepCycles2, which must be positive";
     return "";

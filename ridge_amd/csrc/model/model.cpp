@@ -52,6 +52,10 @@
 //   write stream          = hw.hbmWriteModel 1: C is written at the calibrated
 //                           streaming-write rate, A and B read at the read rate,
 //                           and the two times add (reference: one DRAM rate)
+//   MALL reuse            = hw.mallReuseModel 1: when A and B fit in the MALL,
+//                           HBM supplies them once and the per-XCD re-fetches
+//                           are MALL hits at the calibrated refill rate
+//                           (reference: every L2 miss goes to DRAM)
 //   shared fill           = hw.fillShareModel 1: the resident tiles' first K
 //                           tiles cross from HBM once per distinct panel of an
 //                           XCD (the launch order) and come from the L2s for
@@ -490,6 +494,13 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         const double readBytes = std::max(flops / panelIntensity, (M * K + K * N) * db);
         const double writeBytes = M * N * hw.cBytes;
         double seconds = readBytes / hw.hbmBytesPerSec + writeBytes / hw.hbmWriteBytesPerSec;
+        if (hw.mallReuseModel == 1 && (M * K + K * N) * db <= hw.mallBytes) {
+            // A and B stay in the MALL: HBM supplies each byte once, and the
+            // L2s' further misses (XCDs re-fetching panels) are MALL hits.
+            const double compulsory = (M * K + K * N) * db;
+            seconds = compulsory / hw.hbmBytesPerSec + (readBytes - compulsory) / hw.mallRefillBytesPerSec +
+                      writeBytes / hw.hbmWriteBytesPerSec;
+        }
         if (hw.l2StreamModel == 1) {
             p.l2HitBytes = std::max(0.0, flops / baseIntensity - readBytes);
             seconds += p.l2HitBytes / (hw.l2HitBytesPerCycle * hw.clockHz);

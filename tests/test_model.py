@@ -621,6 +621,39 @@ def test_hbm_write_model_prices_c_at_the_write_rate(tmp_path):
     assert p_on["tEpilogueCycles"] == pytest.approx(2 * p_off["tEpilogueCycles"])
 
 
+def test_mall_reuse_model_serves_refetches_from_the_mall(tmp_path):
+    """mallReuseModel 1 with reads at 8 TB/s, writes at 4 TB/s and MALL hits at
+    2 TB/s, 8 XCDs in the launch order (l2ReuseModel 2): the 256 resident 128x128
+    tiles of 2048 x 2048 x 128 (groupM 8) put 32 tiles on each XCD, 8 row panels
+    by 4 column panels, so the XCDs fetch 8 x 12 x (128 x 128 x 2) = 3,145,728 B
+    of A and B against 1,048,576 compulsory; C is 8,388,608 B. Without the term
+    every fetch is a DRAM read: 3,145,728 / 8e12 + 8,388,608 / 4e12 = 2.490368 us.
+    With it HBM reads each byte once and the other 2,097,152 B are MALL hits:
+    1,048,576 / 8e12 + 2,097,152 / 2e12 + 8,388,608 / 4e12 = 3.2768 us."""
+    base = ', "numXcds": 8, "l2ReuseModel": 2, "hbmWriteModel": 1, "hbmWriteBytesPerSec": 4e12'
+    term = ', "mallReuseModel": 1, "mallRefillBytesPerSec": 2e12, "mallBytes": %d'
+    cfg = dict(M=2048, N=2048, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128,
+               groupM=8)
+    flops = 2.0 * 2048 * 2048 * 128
+    hw = {}
+    for name, extra in (("off", ""), ("on", term % (256 << 20)), ("small", term % 1000000)):
+        f = tmp_path / (name + ".json")
+        f.write_text(_CDNA4_JSON % (base + extra))
+        hw[name] = RM.Hardware(str(f))
+    p_off, p_on, p_small = (RM.predict(hw[n], **cfg) for n in ("off", "on", "small"))
+    assert (p_off["reuseTilesM"], p_off["reuseTilesN"]) == (8.0, 4.0)
+    assert p_off["hbmTFLOPS"] == pytest.approx(flops / 2.490368e-6 / 1e12)
+    assert p_on["hbmTFLOPS"] == pytest.approx(flops / 3.2768e-6 / 1e12)
+    # A and B (1,048,576 B) larger than the MALL: every fetch is a DRAM read again.
+    assert p_small["hbmTFLOPS"] == pytest.approx(p_off["hbmTFLOPS"])
+    # The compute side is untouched.
+    assert p_on["computeTFLOPS"] == pytest.approx(p_off["computeTFLOPS"])
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % (base + ', "mallReuseModel": 1, "mallBytes": 268435456'))
+    with pytest.raises(ValueError, match="mallReuseModel 1"):
+        RM.Hardware(str(bad))
+
+
 def test_fill_latency_model_adds_one_wait_per_round(tmp_path):
     """fillLatencyModel 1 with fillLatencySec 1 us: the prediction's time grows by
     one microsecond per round of one-tile-per-workgroup workgroups (fullWaves)
