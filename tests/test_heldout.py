@@ -137,3 +137,30 @@ def test_third_heldout_figures_as_reported():
     assert base[1]["random"][0] == pytest.approx(25.77, abs=0.01)
     assert base[10]["random"][0] == pytest.approx(3.87, abs=0.01)
     assert all(by_k[1]["mean_regret"] < v[0] for v in base[1].values())
+
+
+# The fourth held-out sweep (data/sweep/mi355x-heldout4.md): the sixteen-term model
+# (the third set's constants plus the MALL reuse term), frozen before measuring.
+REGISTERED4 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout4-registered.csv")
+FROZEN4 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout4-hw.json")
+TABLE4 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout4-table.csv")
+
+
+def test_fourth_heldout_registration():
+    """14 shapes none of the earlier sets or the BASELINE configs hold, against the
+    24-row table; the frozen constants are the third set's plus the MALL reuse
+    term's two keys, nothing else."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED4)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    assert len(held) == 14 and not held & earlier
+    frozen = T.read(TABLE4, require=V.KEY_COLUMNS)
+    keys = [tuple(frozen.number(i, c, int) for c in V.KEY_COLUMNS) for i in range(len(frozen))]
+    assert len(set(keys)) == 24
+    with open(FROZEN3) as a, open(FROZEN4) as b:
+        third, fourth = json.load(a), json.load(b)
+    added = {k: fourth[k] for k in fourth if k not in third}
+    assert added == {"mallReuseModel": 1, "mallBytes": 268435456}
+    assert all(third[k] == fourth[k] for k in third)
