@@ -22,8 +22,7 @@
 //    than the 32x32x16 form: under a full-chip stream of each on random operands
 //    the loaded clock measured 1.89 GHz against 1.65 GHz. With the GEMM's LDS
 //    reads added (probe_mfma_shape.hip) both run at the chip's power ceiling, the
-//    smaller one 0.7% slower on one box and 5.5% faster on another, and the
-//    smaller accumulator tiles keep more of them in registers.
+//    smaller one 0.7% slower on one box and 5.5% faster on another.
 //  * LDS -> VGPR: an MFMA operand is 8 consecutive k of one row (A) or one column
 //    (B) per lane, lane group g = lane/16 holding k = 8g .. 8g+7 and lane%16 the
 //    row or column. A fragments are one `ds_read_b128` per lane. B is stored as
