@@ -41,3 +41,30 @@ def test_a_log_without_the_per_operand_lds_rates_is_refused(tmp_path):
     log = _log_with(tmp_path, line, "")
     with pytest.raises(SystemExit, match="ldsBTrReadBytesPerCycle"):
         calibrate.main(["--from-log", log, "--out", str(tmp_path / "hw.json")])
+
+
+def test_a_second_box_calibration_leaves_the_rankings_unchanged(tmp_path):
+    """The whole calibration run again on a fresh box (mi355x-calibration-box2.txt):
+    its JSON re-derives from its log, its constants sit within 6% of the committed
+    ones, and the pruner's regret at k = 1 and k = 10 on the in-sample sweep, its
+    replicate and the fourth held-out sweep is the same to the hundredth."""
+    import json
+    from ridge_amd import autotune as AT
+    hw = os.path.join(ROOT, "data", "hardware")
+    log2, json2 = os.path.join(hw, "mi355x-calibration-box2.txt"), os.path.join(hw, "mi355x-box2.json")
+    out = tmp_path / "hw2.json"
+    assert calibrate.main(["--from-log", log2, "--out", str(out)]) == 0
+    assert out.read_text() == open(json2).read()
+    a, b = json.load(open(JSON)), json.load(open(json2))
+    assert set(a) == set(b)
+    for key in ("clockHz", "hbmBytesPerSec", "hbmWriteBytesPerSec", "mallRefillBytesPerSec", "loadedClockRatio",
+                "l2HitBytesPerCycle", "smemBytesPerCycle", "mmaCyclesPerInst"):
+        assert abs(b[key] / a[key] - 1.0) < 0.06, key
+    measured = os.path.join(ROOT, "data", "measured")
+    for name in ("mi355x.csv", "mi355x-replicate.csv", "mi355x-heldout4.csv"):
+        sweep = os.path.join(measured, name)
+        ref = {r["k"]: (round(r["mean_regret"], 2), round(r["max_regret"], 2))
+               for r in AT.evaluate(sweep, JSON, ks=(1, 10))[0]}
+        new = {r["k"]: (round(r["mean_regret"], 2), round(r["max_regret"], 2))
+               for r in AT.evaluate(sweep, json2, ks=(1, 10))[0]}
+        assert ref == new, name
