@@ -109,6 +109,36 @@ def test_small_integer_inputs_bit_exact_every_variant(M, N, K):
         assert bad == 0, "%s: %d of %d outputs differ" % (v.label(), bad, M * N)
 
 
+@pytest.mark.parametrize("subnormal", ["A", "B", "C"])
+def test_fp16_subnormal_operands_are_not_flushed(subnormal):
+    """A or B holds FP16 subnormals (integers times 2^-24) and the other operand
+    integers times 2^10; or ("C") both hold integers times 2^-12, so that most
+    outputs are FP16 subnormals. Every product and sum is exact in FP32 and in
+    FP16, so each variant must return the exact product. A matrix unit that
+    flushed subnormal inputs, or an epilogue that flushed subnormal outputs, would
+    return zeros where the reference keeps the values."""
+    M, N, K = 256, 256, 128
+    rng = np.random.default_rng(314)
+    ai = rng.integers(-3, 4, (M, K))
+    bi = rng.integers(-3, 4, (K, N))
+    sa, sb = {"A": (2.0 ** -24, 2.0 ** 10), "B": (2.0 ** 10, 2.0 ** -24), "C": (2.0 ** -12, 2.0 ** -12)}[subnormal]
+    A16, B16 = (ai * sa).astype(np.float16), (bi * sb).astype(np.float16)
+    exact = (ai @ bi) * (sa * sb)
+    want = exact.astype(np.float16)
+    assert np.array_equal(want.astype(np.float64), exact) and np.any(want != 0)
+    tiny = {"A": A16, "B": B16, "C": want}[subnormal]
+    sub = (tiny != 0) & (np.abs(tiny.astype(np.float64)) < 2.0 ** -14)
+    assert (np.all(sub == (tiny != 0)) if subnormal != "C" else sub.mean() > 0.5)
+    A = _to_dev(A16.view(np.uint16).ravel(), (M, K))
+    B = _to_dev(B16.view(np.uint16).ravel(), (K, N))
+    want_bits = want.view(np.uint16).ravel()
+    for v in G.variants():
+        assert v.divides(M, N, K)
+        got = _bits(_run(v.index, A, B, M, N, K))
+        bad = int(np.count_nonzero(got != want_bits))
+        assert bad == 0, "%s, subnormal %s: %d of %d outputs differ" % (v.label(), subnormal, bad, M * N)
+
+
 @pytest.mark.parametrize("key", [(256, 256, 32, 128, 64, 3, 4), (256, 256, 32, 128, 64, 4, 4)])
 def test_headline_4096_exact_integers_and_identity(key):
     """The bench's default variant (s3 g4) and its s4 neighbour at the headline shape."""
