@@ -139,6 +139,38 @@ def test_fp16_subnormal_operands_are_not_flushed(subnormal):
         assert bad == 0, "%s, subnormal %s: %d of %d outputs differ" % (v.label(), subnormal, bad, M * N)
 
 
+def test_inf_nan_and_overflow_follow_ieee():
+    """Special values, every variant. One +inf in A (row 5, k 7) and one NaN in B
+    (k 9, column 11) over small integers: column 11 is NaN; the rest of row 5 is
+    +inf or -inf with the sign of B[7, j], or NaN where B[7, j] = 0 (inf x 0);
+    every other output is the exact integer. A = B = 16 with K = 256 sums to
+    65536, which rounds to +inf in FP16."""
+    M, N, K = 256, 256, 128
+    rng = np.random.default_rng(2718)
+    ai = rng.integers(-3, 4, (M, K)).astype(np.float64)
+    bi = rng.integers(-3, 4, (K, N)).astype(np.float64)
+    finite = ai @ bi
+    a16, b16 = ai.astype(np.float16), bi.astype(np.float16)
+    a16[5, 7] = np.inf
+    b16[9, 11] = np.nan
+    want = finite.astype(np.float16)
+    want[5, :] = np.where(bi[7] > 0, np.inf, np.where(bi[7] < 0, -np.inf, np.nan))
+    want[:, 11] = np.nan
+    A = _to_dev(a16.view(np.uint16).ravel(), (M, K))
+    B = _to_dev(b16.view(np.uint16).ravel(), (K, N))
+    Kb = 256
+    big = torch.full((M, Kb), 16.0, dtype=torch.float16, device=DEV)
+    bigB = torch.full((Kb, N), 16.0, dtype=torch.float16, device=DEV)
+    for v in G.variants():
+        got = _bits(_run(v.index, A, B, M, N, K)).view(np.float16).reshape(M, N)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), "%s: NaN positions differ" % v.label()
+        assert np.array_equal(got[~nan].view(np.uint16), want[~nan].view(np.uint16)), (
+            "%s: %d finite or infinite outputs differ" % (v.label(), int(np.count_nonzero(got[~nan] != want[~nan]))))
+        over = _bits(_run(v.index, big, bigB, M, N, Kb)).view(np.float16)
+        assert np.all(np.isposinf(over)), "%s: 65536 did not round to +inf" % v.label()
+
+
 @pytest.mark.parametrize("key", [(256, 256, 32, 128, 64, 3, 4), (256, 256, 32, 128, 64, 4, 4)])
 def test_headline_4096_exact_integers_and_identity(key):
     """The bench's default variant (s3 g4) and its s4 neighbour at the headline shape."""
