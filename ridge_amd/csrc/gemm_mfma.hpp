@@ -42,7 +42,8 @@
 //    output tiles that shares A and B panels in its L2.
 //
 // Preconditions (checked by the host launcher, never by the kernel): M % BM ==
-// N % BN == K % BK == 0 and K >= BK; 16-byte aligned A, B, C.
+// N % BN == K % BK == 0 and K >= BK; BM * K, BK * N and the tile count below 2^31
+// (tile offsets are 32-bit); 16-byte aligned A, B, C.
 #pragma once
 
 #include <hip/hip_runtime.h>
