@@ -139,6 +139,28 @@ def test_fp16_subnormal_operands_are_not_flushed(subnormal):
         assert bad == 0, "%s, subnormal %s: %d of %d outputs differ" % (v.label(), subnormal, bad, M * N)
 
 
+def test_python_gemm_on_offset_views():
+    """gemm() on contiguous views that start inside a larger buffer: a 16-byte
+    aligned start gives the same bits as a fresh tensor; a start 2 bytes off is
+    refused by the launcher (hipErrorInvalidValue) and raised, never launched."""
+    M, N, K = 256, 256, 128
+    Ab, Bb, want = _exact_case(M, N, K, -3, 3, 99)
+    A = _to_dev(Ab.ravel(), (M, K))
+    B = _to_dev(Bb.ravel(), (K, N))
+    idx = G.find_variant(256, 256, 32, 128, 64, 3, 4)
+    for offset, ok in ((8, True), (1, False)):
+        buf = torch.zeros(M * K + 64, dtype=torch.float16, device=DEV)
+        view = buf[offset:offset + M * K].view(M, K)
+        view.copy_(A)
+        if ok:
+            C = G.gemm(view, B, idx)
+            torch.cuda.synchronize()
+            assert np.array_equal(_bits(C), want)
+        else:
+            with pytest.raises(G.RidgeGemmError, match="hipError 1"):
+                G.gemm(view, B, idx)
+
+
 def test_inf_nan_and_overflow_follow_ieee():
     """Special values, every variant. One +inf in A (row 5, k 7) and one NaN in B
     (k 9, column 11) over small integers: column 11 is NaN; the rest of row 5 is
