@@ -241,9 +241,10 @@ def cpu_threads():
     return max(1, min(n, MAX_CPU_THREADS))
 
 
-def measured_traffic(M, N, K, key):
+def measured_traffic(M, N, K, key, cold=False):
     """HBM bytes per launch from the committed rocprofv3 traffic summary for this
-    shape and variant, or None when no profile covers it."""
+    shape and variant (its cold-rotation figure with cold=True), or None when no
+    profile covers it."""
     if not os.path.isdir(PROFILES):
         return None
     for name in sorted(os.listdir(PROFILES)):
@@ -252,7 +253,7 @@ def measured_traffic(M, N, K, key):
         with open(os.path.join(PROFILES, name)) as f:
             t = json.load(f)
         if tuple(t.get("shape", ())) == (M, N, K) and tuple(t.get("variant", ())) == key:
-            return t.get("hbm_bytes_per_launch")
+            return t.get("cold_hbm_bytes_per_launch" if cold else "hbm_bytes_per_launch")
     return None
 
 
@@ -564,7 +565,7 @@ def main():
                 "spread": window_summary(flops, cold_windows),
                 "sets": n_sets, "set_bytes": set_bytes, "launches_per_window": cold_steps,
                 "rotation_warm_seconds": cold_warm_s,
-                "roofline": roofline(M, N, K, cold_ms, None)}
+                "roofline": roofline(M, N, K, cold_ms, measured_traffic(M, N, K, key, cold=True))}
         if blas is not None:
             try:
                 blas = G.BlasLt()
