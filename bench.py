@@ -3,11 +3,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--repeats R] [--variant BM,BN,BK,WM,WN,S,G]
                     [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt] [--no-cold]
-                    [--operands uniform|zeros|ones]
                     [--allow-partitioned]
     python bench.py --mode copy     # plain device copy of known size, for scaling
                                     # rocprofv3 FETCH_SIZE / WRITE_SIZE counters
-    python bench.py --mode cold-split --steps 200   # which operand's cold lines cost a launch
 
 A step is one C = A * B launch (FP16 A, B row-major from a seeded U[-1,1) device
 fill, FP32 accumulate, FP16 C) through the C ABI, with inputs resident in HBM
@@ -367,60 +365,6 @@ def run_copy_mode(steps):
     print(json.dumps({"mode": "copy", "bytes_per_copy": nbytes, "copies": steps}))
 
 
-def run_cold_split(args):
-    """Which operand's cold lines cost a launch: the GEMM (and hipBLASLt) timed
-    over 7 operand sets with only C, only A, only B, A and B, or all three rotated,
-    against one re-used set. Each figure is the middle of --repeats windows of
-    --steps launches after 1.5 s of the same rotation. Prints one JSON line (a
-    diagnostic, not the metric)."""
-    import torch
-    from ridge_amd import gemm as G
-    M, N, K = parse_ints(args.shape, 3)
-    idx = G.find_variant(*parse_ints(args.variant, 7))
-    if idx < 0 or not G.variant(idx).divides(M, N, K):
-        raise SystemExit("variant %s is not in the table or does not divide the shape" % args.variant)
-    stream = torch.cuda.current_stream()
-    n = 7
-    A = [torch.empty((M, K), dtype=torch.float16, device="cuda:0") for _ in range(n)]
-    B = [torch.empty((K, N), dtype=torch.float16, device="cuda:0") for _ in range(n)]
-    C = [torch.empty((M, N), dtype=torch.float16, device="cuda:0") for _ in range(n)]
-    for i in range(n):
-        if args.operands == "uniform":
-            G.fill_uniform(A[i], 1 + 2 * i)
-            G.fill_uniform(B[i], 2 + 2 * i)
-        else:
-            A[i].fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
-            B[i].fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
-    torch.cuda.synchronize()
-    blas = G.BlasLt()
-    blas.prepare(A[0], B[0], C[0], M, N, K, candidates=16, iters=20, stream=stream)
-    kernels = {"ridge": lambda a, b, c: G.bound_launch(idx, a, b, c, M, N, K, stream),
-               "hipblaslt": lambda a, b, c: blas.bound_gemm(a, b, c, M, N, K, stream=stream)}
-    picks = {"warm": lambda i: (A[0], B[0], C[0]), "c_rotated": lambda i: (A[0], B[0], C[i % n]),
-             "a_rotated": lambda i: (A[i % n], B[0], C[0]), "b_rotated": lambda i: (A[0], B[i % n], C[0]),
-             "ab_rotated": lambda i: (A[i % n], B[i % n], C[0]), "all_rotated": lambda i: (A[i % n], B[i % n], C[i % n])}
-    out = {"mode": "cold-split", "shape": [M, N, K], "variant": G.variant(idx).label(), "sets": n,
-           "operands": args.operands,
-           "launches_per_window": args.steps, "windows": max(1, args.repeats), "us_per_launch": {}}
-    for kname, bind in kernels.items():
-        for pname, pick in picks.items():
-            calls = [bind(*pick(i)) for i in range(n)]
-            count = [0]
-
-            def step():
-                calls[count[0] % n]()
-                count[0] += 1
-            t0 = time.perf_counter()
-            while time.perf_counter() - t0 < 1.5:
-                for _ in range(n):
-                    step()
-                torch.cuda.synchronize()
-            _, event_ms = time_windows(step, args.steps, stream, max(1, args.repeats))
-            out["us_per_launch"]["%s/%s" % (kname, pname)] = round(middle(event_ms) * 1e3, 3)
-    blas.close()
-    print(json.dumps(out), flush=True)
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -428,8 +372,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--variant", default=",".join(str(x) for x in DEFAULT_VARIANT))
     ap.add_argument("--shape", default=",".join(str(x) for x in DEFAULT_SHAPE))
-    ap.add_argument("--operands", default="uniform", choices=["uniform", "zeros", "ones"],
-                    help="operand data; anything but the default is a power-limit probe, not the metric")
     ap.add_argument("--warm-seconds", type=float, default=5.0)
     ap.add_argument("--cold-warm-seconds", type=float, default=2.0,
                     help="seconds the cold rotation runs before its windows are timed (capped by --warm-seconds)")
@@ -439,7 +381,7 @@ def main():
     ap.add_argument("--no-blaslt", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--allow-partitioned", action="store_true")
-    ap.add_argument("--mode", default="gemm", choices=["gemm", "copy", "cold-split"])
+    ap.add_argument("--mode", default="gemm", choices=["gemm", "copy"])
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -452,10 +394,6 @@ def main():
         raise SystemExit("bench.py needs a GPU")
     if args.mode == "copy":
         run_copy_mode(max(args.steps, 1))
-        return
-    if args.mode == "cold-split":
-        device_check(args.allow_partitioned)
-        run_cold_split(args)
         return
     device = device_check(args.allow_partitioned)
 
@@ -476,14 +414,8 @@ def main():
     B = torch.empty((K, N), dtype=torch.float16, device=dev)
     C = torch.empty((M, N), dtype=torch.float16, device=dev)
     def fill(a, b):
-        if args.operands == "uniform":
-            G.fill_uniform(a, 1)
-            G.fill_uniform(b, 2)
-        else:
-            # Constant operands toggle no bits from one MFMA to the next; the
-            # same instructions then draw less power (1/64 keeps C exact).
-            a.fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
-            b.fill_(0.0 if args.operands == "zeros" else 1.0 / 64)
+        G.fill_uniform(a, 1)
+        G.fill_uniform(b, 2)
 
     fill(A, B)
     torch.cuda.synchronize()
@@ -599,10 +531,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": ("synthetic: A, B ~ U[-1,1) FP16 from splitmix64 seeds 1 and 2, generated on the device"
-                 if args.operands == "uniform" else
-                 "POWER-LIMIT PROBE, not the metric: every element of A and B is %s"
-                 % ("0" if args.operands == "zeros" else "1/64")),
+        "data": "synthetic: A, B ~ U[-1,1) FP16 from splitmix64 seeds 1 and 2, generated on the device",
         "config": {"workload": "FP16 GEMM M=%d N=%d K=%d, row-major A/B/C, FP32 accumulate, FP16 C" % (M, N, K),
                    "variant": v.label(), "parallelism": "single GPU"},
         "repeats": repeats,

@@ -36,6 +36,7 @@ import statistics
 import sys
 
 from ridge_amd import model as RM
+from ridge_amd.rocprof import counter_value, parse_counter_dir, parse_trace_dir  # noqa: F401
 from ridge_amd import tables as T
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -261,35 +262,6 @@ def _template_args(name):
     return tuple(int(x) for x in vals)
 
 
-def _find(directory, suffix):
-    hits = sorted(glob.glob(os.path.join(directory, "**", "*" + suffix), recursive=True))
-    if not hits:
-        raise SystemExit("no *%s under %s" % (suffix, directory))
-    return hits
-
-
-def parse_counter_dir(directory):
-    """{dispatch_id: {"name": kernel, "counters": {name: [values]}}} for every
-    dispatch of every *counter_collection.csv under `directory`."""
-    out = {}
-    for path in _find(directory, "counter_collection.csv"):
-        with open(path) as f:
-            for r in csv.DictReader(f):
-                d = out.setdefault((path, int(r["Dispatch_Id"])), {"name": r["Kernel_Name"], "counters": {}})
-                d["counters"].setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
-    return out
-
-
-def parse_trace_dir(directory):
-    out = {}
-    for path in _find(directory, "kernel_trace.csv"):
-        with open(path) as f:
-            for r in csv.DictReader(f):
-                out[(path, int(r["Dispatch_Id"]))] = {
-                    "name": r["Kernel_Name"], "ns": float(r["End_Timestamp"]) - float(r["Start_Timestamp"])}
-    return out
-
-
 def gemm_dispatches(parsed, configs, launches):
     """The GEMM dispatches in dispatch order, grouped per config (`launches` per
     config, twice that for a registration with a long factor: the K launches
@@ -310,14 +282,10 @@ def gemm_dispatches(parsed, configs, launches):
 
 
 def _counter(dispatch, name, xcds, grbm):
-    vals = dispatch["counters"].get(name)
-    if vals is None:
-        raise SystemExit("counter %s missing from a dispatch" % name)
-    if grbm:
-        # One value per XCD (reported separately or summed): the per-XCD clock
-        # count is the max, or the sum over the XCDs divided by their number.
-        return max(vals) if len(vals) > 1 else vals[0] / xcds
-    return sum(vals)
+    # GRBM_* clock counts are per XCD (rocprof.counter_value); every other
+    # counter of a dispatch is summed over its instances.
+    del grbm
+    return counter_value(dispatch, name, xcds)
 
 
 def cmd_gather(args):

@@ -37,10 +37,6 @@ def _bits(t):
     return t.cpu().view(torch.int16).numpy().view(np.uint16).ravel()
 
 
-def _max_abs(bits):
-    return float(np.abs(bits.view(np.float16).astype(np.float64)).max())
-
-
 def _run(i, A, B, M, N, K):
     C = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
     rc = G.launch(i, A, B, C, M, N, K)
@@ -416,6 +412,46 @@ def _max_abs(bits):
     """max |x| over FP16 bit patterns (the reference's normalisation,
     check-gemm.cu:110-135, taken from the operands actually used)."""
     return float(np.max(np.abs(O.f16_bits_to_f32(bits))))
+
+
+# The best row of each BASELINE config other than the headline (whose every
+# output the test above checks). The persistent rows start each output tile's K
+# loop at a tile-dependent K tile and wrap, so their FP32 sums round in another
+# order than the other rows'; small-integer inputs (exact sums) cannot see that.
+REPORTED_ROWS = [
+    ((1024, 1024, 1024), (64, 64, 64, 32, 32, 4, 8)),
+    ((8192, 8192, 128), (256, 128, 32, 64, 64, 6, 4)),
+    ((16384, 128, 8192), (64, 128, 128, 32, 64, 3, 8)),
+]
+
+
+@pytest.mark.parametrize("shape,key", REPORTED_ROWS, ids=["1024cube", "8192sq_k128", "tall_skinny"])
+def test_reported_rows_every_output(shape, key):
+    """Every output of the reported row on U[-1,1) inputs against the f64 oracle,
+    under the reference's gates (bench/check-gemm.cu:277-322 compares the whole C)
+    and the FP16-output gate (each element within FP32 accumulation plus one
+    rounding)."""
+    M, N, K = shape
+    idx = G.find_variant(*key)
+    assert idx >= 0, key
+    print("reported row %s at %dx%dx%d, every output" % (G.variant(idx).label(), M, N, K), flush=True)
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, 1)
+    G.fill_uniform(B, 2)
+    Ab, Bb = _bits(A), _bits(B)
+    got = O.f16_bits_to_f32(_bits(_run(idx, A, B, M, N, K))).reshape(M, N)
+    del A, B
+    torch.cuda.empty_cache()
+    ref = O.gemm_f64(Ab, Bb, M, N, K)
+    ok, frob, mx, ne = O.passes(got, ref, _max_abs(Ab), _max_abs(Bb), K)
+    print("  reference gates: frob %.3e maxRel %.3e norm %.3e" % (frob, mx, ne), flush=True)
+    assert ok, "reference gates: frob %.3e maxRel %.3e norm %.3e" % (frob, mx, ne)
+    absprod = O.gemm_f64(O.abs_bits(Ab), O.abs_bits(Bb), M, N, K)
+    ok, frob, worst = O.passes_fp16(got, ref, absprod, K)
+    print("  FP16-output gate over %d outputs: frob %.3e, worst element at %.3f of its bound"
+          % (M * N, frob, worst), flush=True)
+    assert ok, "FP16-output gate: frob %.3e, worst element at %.2f of its bound" % (frob, worst)
 
 
 def test_hipblaslt_comparator_agrees_with_oracle():
