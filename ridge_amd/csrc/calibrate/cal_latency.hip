@@ -10,6 +10,14 @@
 // as in the reference. Waves 16 with ILP 8 is omitted: its accumulators
 // (8 x 16 per lane) plus fragments exceed the 128 registers a lane may hold at
 // four waves per SIMD.
+//
+// The bench also times the launch floor: back-to-back launches of a kernel
+// whose workgroups each store one word, over grids of 64 to 4096 workgroups of
+// 256 and 512 workitems, on one stream with HIP events. That per-launch time is
+// what a kernel boundary costs a sequence of launches before any work (queue
+// processing, workgroup dispatch, completion signal); launchSeconds is its value
+// at 256 workgroups of 256 workitems, launchSecondsPerWorkgroup the slope of a
+// least-squares line through the 256-workitem grids.
 #include "cal_common.hpp"
 #include "gemm_mfma.hpp"
 
@@ -62,6 +70,34 @@ __global__ __launch_bounds__(Waves * 64) void readMfmaKernel(int iters, float* s
     for (int j = 0; j < Ilp; ++j) s += acc[j][0] + acc[j][15];
     if (s == -1.0e38f) sink[0] = s;
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
+}
+
+__global__ __launch_bounds__(512) void launchProbeKernel(float* sink) {
+    if (threadIdx.x == 0) sink[blockIdx.x] = float(blockIdx.x);
+}
+
+// Per-launch seconds of `launches` back-to-back launches of launchProbeKernel
+// (grid x threads), middle of kRepeats windows.
+double launchSeconds(int grid, int threads, float* dSink, int launches) {
+    hipEvent_t e0, e1;
+    CAL_HIP_CHECK(hipEventCreate(&e0));
+    CAL_HIP_CHECK(hipEventCreate(&e1));
+    std::vector<double> w;
+    for (int r = 0; r < kRepeats; ++r) {
+        CAL_HIP_CHECK(hipDeviceSynchronize());
+        CAL_HIP_CHECK(hipEventRecord(e0, nullptr));
+        for (int i = 0; i < launches; ++i)
+            hipLaunchKernelGGL(launchProbeKernel, dim3(grid), dim3(threads), 0, nullptr, dSink);
+        CAL_HIP_CHECK(hipGetLastError());
+        CAL_HIP_CHECK(hipEventRecord(e1, nullptr));
+        CAL_HIP_CHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        CAL_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        w.push_back(ms * 1e-3 / launches);
+    }
+    CAL_HIP_CHECK(hipEventDestroy(e0));
+    CAL_HIP_CHECK(hipEventDestroy(e1));
+    return middle(w);
 }
 
 template <int Waves, int Ilp>
@@ -147,6 +183,36 @@ int main() {
     reportConstant("warpsNeededToHide", double(needed[1]), "waves/CU", reps[1][wBest]);
     std::printf("  the reported constant is the ILP=2 column, a threshold on a smooth curve\n");
     std::printf("\nCAL_RESULT warpsNeededToHide %d\n", needed[1]);
+
+    // The launch floor.
+    constexpr int kGrids[] = {64, 128, 256, 512, 1024, 2048, 4096};
+    constexpr int kLaunches = 2000;
+    float* dLaunchSink = nullptr;
+    CAL_HIP_CHECK(hipMalloc(&dLaunchSink, 4096 * sizeof(float)));
+    launchSeconds(256, 256, dLaunchSink, kLaunches);  // first launches load the code object
+    std::printf("\nlaunch floor: back-to-back launches of a kernel that stores one word per workgroup\n");
+    std::printf("  %9s %14s %14s\n", "workgroups", "256 items (us)", "512 items (us)");
+    double sx = 0.0, sy = 0.0, sxx = 0.0, sxy = 0.0, at256 = 0.0;
+    int n = 0;
+    for (int g : kGrids) {
+        const double t256 = launchSeconds(g, 256, dLaunchSink, kLaunches);
+        const double t512 = launchSeconds(g, 512, dLaunchSink, kLaunches);
+        std::printf("  %9d %14.3f %14.3f\n", g, t256 * 1e6, t512 * 1e6);
+        std::printf("CAL_INFO launchSeconds_wg%d_items256 %.6e\n", g, t256);
+        std::printf("CAL_INFO launchSeconds_wg%d_items512 %.6e\n", g, t512);
+        if (g == 256) at256 = t256;
+        if (g >= 256) {
+            sx += g;
+            sy += t256;
+            sxx += double(g) * g;
+            sxy += g * t256;
+            ++n;
+        }
+    }
+    const double slope = (n * sxy - sx * sy) / (n * sxx - sx * sx);
+    std::printf("CAL_RESULT launchSeconds %.6e\n", at256);
+    std::printf("CAL_RESULT launchSecondsPerWorkgroup %.6e\n", slope);
+    CAL_HIP_CHECK(hipFree(dLaunchSink));
     CAL_HIP_CHECK(hipFree(dSink));
     CAL_HIP_CHECK(hipFree(dStamps));
     return 0;

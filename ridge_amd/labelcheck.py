@@ -48,10 +48,13 @@ class Registration:
     data/hardware/mi355x.json at registration time and `sources` frozen copies
     of the measured rows the selection was made from, so a later re-calibration
     or re-measurement cannot change the registered configs or thresholds.
-    `long_factor` F > 0 adds LAUNCHES launches of every config at K x F."""
+    `factors(config)` lists the K multipliers every config is launched at
+    (LAUNCHES launches each, the multiplier 1 first): registration 2 adds K x 16
+    (`long_factor`), the design set K / 2 (where BK divides it) and K x 2."""
 
-    def __init__(self, number, stem, long_factor):
+    def __init__(self, number, stem, long_factor=0, factors=None):
         self.number = number
+        self.stem = stem
         self.mapping = os.path.join(SWEEP_DIR, stem + "-mapping.md")
         self.hw_json = os.path.join(SWEEP_DIR, stem + "-hw.json")
         self.sources = [os.path.join(SWEEP_DIR, stem + "-sweep.csv"),
@@ -59,9 +62,29 @@ class Registration:
         self.configs = os.path.join(SWEEP_DIR, stem + "-configs.csv")
         self.counters = os.path.join(ROOT, "data", "measured", stem.replace("rocprof-label", "rocprof-labels") + ".csv")
         self.long_factor = long_factor
+        self._factors = factors
+
+    def factors(self, c):
+        if self._factors is not None:
+            return self._factors(c)
+        return [1, self.long_factor] if self.long_factor else [1]
+
+    def duration_column(self, f):
+        if f == 1:
+            return "duration_ns"
+        if f == self.long_factor:
+            return "long_duration_ns"
+        return "duration_x%g_ns" % f
 
 
-REGISTRATIONS = {1: Registration(1, "rocprof-label", 0), 2: Registration(2, "rocprof-label2", 16)}
+def design_factors(c):
+    """K / 2 where it is a whole number of K tiles, and K x 2."""
+    half = c["K"] // 2
+    return [1] + ([0.5] if c["K"] % 2 == 0 and half % c["BK"] == 0 and half >= c["BK"] else []) + [2]
+
+
+REGISTRATIONS = {1: Registration(1, "rocprof-label", 0), 2: Registration(2, "rocprof-label2", 16),
+                 "design": Registration("design", "rocprof-label-design", factors=design_factors)}
 CURRENT = 2
 # Registration 1's files under their original names (kept for its tests).
 HW_JSON = REGISTRATIONS[1].hw_json
@@ -182,6 +205,51 @@ def select_configs(sources=SOURCES, hw_json=HW_JSON, per_label=PER_LABEL, regist
     return out
 
 
+def design_configs():
+    """The label-design set: in-sample rows the decision rules and the model's
+    counter predictions are developed on, never scored. Every config of
+    registrations 1 and 2 whose variant is still in the kernel table; for each
+    of the 14 in-sample sweep shapes (data/measured/mi355x.csv) its fastest,
+    median and slowest measured row; and the fastest row of each BASELINE config
+    (data/measured/mi355x-baseline-configs.csv). Configs are keyed by shape and
+    tile; the first occurrence is kept."""
+    from ridge_amd import validate as V
+    table = set(V.kernel_table_keys())
+    hw = RM.Hardware(os.path.join(ROOT, "data", "hardware", "mi355x.json"))
+    measured = {}
+    for name in ("mi355x.csv", "mi355x-baseline-configs.csv"):
+        for r in _read_rows(os.path.join(ROOT, "data", "measured", name)):
+            measured.setdefault(_key(r), r)
+    out, seen = [], set()
+
+    def add(r, why):
+        key = _key(r)
+        if key in seen or tuple(int(r[k]) for k in KEY_FIELDS) not in table:
+            return
+        seen.add(key)
+        m = measured.get(key, r)
+        row = dict(m)
+        p = predict_row(hw, row, True)
+        out.append(_config_row("DESIGN", row, p, why))
+
+    for reg in (1, 2):
+        for c in _read_rows(REGISTRATIONS[reg].configs):
+            key = _key(c)
+            if key in measured:
+                add(measured[key], "registration %d config" % reg)
+    sweep = _read_rows(os.path.join(ROOT, "data", "measured", "mi355x.csv"))
+    for shape in sorted({(int(r["M"]), int(r["N"]), int(r["K"])) for r in sweep}):
+        rows = sorted((r for r in sweep if (int(r["M"]), int(r["N"]), int(r["K"])) == shape),
+                      key=lambda r: (-float(r["tflops"]),) + tuple(int(r[k]) for k in KEY_FIELDS))
+        for pos, why in ((0, "fastest"), (len(rows) // 2, "median"), (len(rows) - 1, "slowest")):
+            add(rows[pos], "in-sample shape, %s row" % why)
+    base = _read_rows(os.path.join(ROOT, "data", "measured", "mi355x-baseline-configs.csv"))
+    for shape in sorted({(int(r["M"]), int(r["N"]), int(r["K"])) for r in base}):
+        rows = [r for r in base if (int(r["M"]), int(r["N"]), int(r["K"])) == shape]
+        add(max(rows, key=lambda r: float(r["tflops"])), "BASELINE config, fastest row")
+    return out
+
+
 CONFIG_COLUMNS = ["predicted_label", "model_label", "tag", "M", "N", "K"] + KEY_FIELDS + \
     ["regsPerThread", "theoretical_waves_per_cu", "pred_tflops", "measured_tflops"]
 CONFIG_COLUMNS_2 = CONFIG_COLUMNS + ["schedule", "why"]
@@ -189,10 +257,15 @@ CONFIG_COLUMNS_2 = CONFIG_COLUMNS + ["schedule", "why"]
 
 def cmd_select(args):
     reg = REGISTRATIONS[args.registration]
-    rows = select_configs(reg.sources, reg.hw_json, registration=reg.number)
-    cols = CONFIG_COLUMNS_2 if reg.number == 2 else CONFIG_COLUMNS
+    if reg.number == "design":
+        rows = design_configs()
+        note = "label-design set (in-sample, never scored); see ridge_amd/labelcheck.py design_configs"
+    else:
+        rows = select_configs(reg.sources, reg.hw_json, registration=reg.number)
+        note = "registered before any rocprofv3 run; see %s" % os.path.relpath(reg.mapping, ROOT)
+    cols = CONFIG_COLUMNS if reg.number == 1 else CONFIG_COLUMNS_2
     out = args.out or reg.configs
-    T.write(out, cols, rows, ["registered before any rocprofv3 run; see %s" % os.path.relpath(reg.mapping, ROOT)])
+    T.write(out, cols, rows, [note])
     for r in rows:
         print("%-9s %-28s %6dx%-6dx%-5d %dx%dx%d w%dx%d s%d g%d %s" % (
             r["predicted_label"], r["tag"], r["M"], r["N"], r["K"], *[r[k] for k in KEY_FIELDS], r.get("why", "")))
@@ -222,8 +295,8 @@ def cmd_run(args):
             raise SystemExit("config %d: variant not in the kernel table (a row retired after the "
                              "registration; its counters were gathered and scored before, and a replay "
                              "needs the table of the registration commit)" % i)
-        for factor in ([1, reg.long_factor] if reg.long_factor else [1]):
-            M, N, K = c["M"], c["N"], c["K"] * factor
+        for factor in reg.factors(c):
+            M, N, K = c["M"], c["N"], int(c["K"] * factor)
             if not G.variant(idx).divides(M, N, K):
                 raise SystemExit("config %d: variant does not divide %dx%dx%d" % (i, M, N, K))
             print("config %d/%d %s %dx%dx%d %s" % (i + 1, len(configs), c["predicted_label"], M, N, K,
@@ -241,9 +314,8 @@ def cmd_run(args):
                     raise SystemExit("config %d: launch returned %d" % (i, rc))
                 torch.cuda.synchronize()
             del A, B, C
-    print("labelcheck run: %d configs x %d launches%s" % (
-        len(configs), args.launches, " (and as many at K x %d)" % reg.long_factor if reg.long_factor else ""),
-        flush=True)
+    print("labelcheck run: %d configs x %d launches at each of their K multipliers" % (len(configs), args.launches),
+          flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -263,15 +335,19 @@ def _template_args(name):
 
 
 def gemm_dispatches(parsed, configs, launches):
-    """The GEMM dispatches in dispatch order, grouped per config (`launches` per
-    config, twice that for a registration with a long factor: the K launches
-    first); each name must carry that config's template arguments."""
+    """The GEMM dispatches in dispatch order, grouped per config: `launches`
+    dispatches per config (an int for all, or one count per config, as when
+    configs are launched at different numbers of K multipliers); each name must
+    carry that config's template arguments."""
+    counts = [launches] * len(configs) if isinstance(launches, int) else list(launches)
     gemm = [(k, v) for k, v in sorted(parsed.items()) if _GEMM_NAME.search(v["name"])]
-    if len(gemm) != len(configs) * launches:
-        raise SystemExit("expected %d GEMM dispatches, found %d" % (len(configs) * launches, len(gemm)))
+    if len(gemm) != sum(counts):
+        raise SystemExit("expected %d GEMM dispatches, found %d" % (sum(counts), len(gemm)))
     groups = []
+    at = 0
     for i, c in enumerate(configs):
-        chunk = gemm[i * launches:(i + 1) * launches]
+        chunk = gemm[at:at + counts[i]]
+        at += counts[i]
         want = tuple(c[k] for k in KEY_FIELDS)
         for _, v in chunk:
             got = _template_args(v["name"])
@@ -294,14 +370,18 @@ def cmd_gather(args):
     with open(reg.hw_json) as f:
         hwj = json.load(f)
     xcds = int(hwj.get("numXcds", 8))
-    per = args.launches * (2 if reg.long_factor else 1)
+    facs = [reg.factors(c) for c in configs]
+    per = [args.launches * len(f) for f in facs]
     p1 = gemm_dispatches(parse_counter_dir(args.counters), configs, per)
     pf = gemm_dispatches(parse_counter_dir(args.fetch), configs, per)
     pw = gemm_dispatches(parse_counter_dir(args.write), configs, per)
     pt = gemm_dispatches(parse_trace_dir(args.trace), configs, per)
     n = args.launches
     rows = []
-    cols = CONFIG_COLUMNS_2 if reg.number == 2 else CONFIG_COLUMNS
+    cols = CONFIG_COLUMNS if reg.number == 1 else CONFIG_COLUMNS_2
+    dcols = []
+    for f in facs:
+        dcols += [reg.duration_column(x) for x in f if reg.duration_column(x) not in dcols]
     for i, c in enumerate(configs):
         med = lambda xs: statistics.median(xs)  # noqa: E731
         row = {k: c[k] for k in cols}
@@ -309,9 +389,10 @@ def cmd_gather(args):
             row[name] = med([_counter(d, name, xcds, name.startswith("GRBM_")) for d in p1[i][:n]])
         row["FETCH_SIZE"] = med([_counter(d, "FETCH_SIZE", xcds, False) for d in pf[i][:n]])
         row["WRITE_SIZE"] = med([_counter(d, "WRITE_SIZE", xcds, False) for d in pw[i][:n]])
-        row["duration_ns"] = med([d["ns"] for d in pt[i][:n]])
-        if reg.long_factor:
-            row["long_duration_ns"] = med([d["ns"] for d in pt[i][n:]])
+        for col in dcols:
+            row[col] = ""
+        for j, f in enumerate(facs[i]):
+            row[reg.duration_column(f)] = med([d["ns"] for d in pt[i][j * n:(j + 1) * n]])
         rows.append(row)
     out = args.out or reg.counters
     T.write(out, list(rows[0].keys()), rows,
@@ -458,7 +539,8 @@ def cmd_score(args):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--registration", type=int, default=CURRENT, choices=sorted(REGISTRATIONS))
+    ap.add_argument("--registration", type=lambda x: x if x == "design" else int(x), default=CURRENT,
+                    choices=list(REGISTRATIONS))
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("select")
     s.add_argument("--out", default=None)
