@@ -119,6 +119,16 @@ struct HardwareModel {
                                      // 1: the resident workgroups' first tiles come from HBM once per
                                      //    distinct panel an XCD holds (the kernels' launch order) and
                                      //    from the L2s for the rest, at l2HitBytesPerCycle
+    int launchModel = 0;             // 0: a launch costs its work alone (reference)
+                                     // 1: a kernel boundary adds launchOverheadSeconds to each launch of a
+                                     //    back-to-back sequence (the measurement protocol of the sweeps)
+    double launchOverheadSeconds = 0.0;  // [CAL] per launch on top of its work, back to back (cal-latency)
+    double launchIsolatedSeconds = 0.0;  // [CAL] the same for one launch from an idle stream (cal-latency)
+    int labelModel = 0;              // 0: the label names the derating furthest from 1 (reference :129-143)
+                                     // 1: the label is the counter decision table applied to the model's
+                                     //    own prediction of what the counters read on one launch from an
+                                     //    idle stream: DRAM share, body share from a second K, CU share,
+                                     //    LDS and MFMA busy shares (Prediction's observable fields)
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -63,6 +63,17 @@ struct Prediction {
     double refillMissShare = 0.0;      // share of the tile refill that misses the L2 (mallStreamModel 1)
     double mallLoad = 0.0;             // load that stream puts on the MALL path (mallStreamModel 1)
     double mallStretch = 1.0;          // K-step stretch read off the calibrated curve (mallStreamModel 1)
+
+    // What the counters read on one launch from an idle stream (labelModel 1; 0 otherwise).
+    double kernelSeconds = 0.0;        // duration of that launch
+    double dramReadBytes = 0.0;        // bytes the L2s miss (MALL hits included), A and B
+    double dramWriteBytes = 0.0;       // C
+    double dramShare = 0.0;            // read bytes at the read rate + C at the write rate, over the duration
+    double bodyFactor = 0.0;           // the second K of the body share, as a multiple of K (1/2 or 2)
+    double bodyShare = 0.0;            // share of the duration that scales with K, from the two durations
+    double cuShare = 0.0;              // CU-time share the grid keeps occupied
+    double mfmaShare = 0.0;            // matrix-pipe busy share of the SIMD cycles
+    double ldsShare = 0.0;             // LDS busy share of the CU cycles (fragment reads)
 };
 
 }  // namespace ridge

@@ -48,6 +48,9 @@ typedef struct ridge_model_prediction {
     double refillMissShare;  /* share of the tile refill that misses the L2 (mallStreamModel 1) */
     double mallLoad;         /* load that stream puts on the MALL path (mallStreamModel 1) */
     double mallStretch;      /* K-step stretch from the calibrated curve (mallStreamModel 1) */
+    /* What the counters read on one launch from an idle stream (labelModel 1; 0 otherwise). */
+    double kernelSeconds, dramReadBytes, dramWriteBytes, dramShare, bodyFactor, bodyShare, cuShare, mfmaShare,
+        ldsShare;
 } ridge_model_prediction_t;
 
 /* Default config (the reference's GemmConfig defaults, config.h:18-39). */

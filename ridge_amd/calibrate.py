@@ -122,6 +122,13 @@ def band_check(res, spec):
                     res["l2HitBytesPerCycle"] * res["clockHz"] / 1e12, "TB/s",
                     "L2-missing refill path: below what the L2s serve")
         ok &= check("mallStretch0", res["mallStretch0"], 0.95, 1.05, "x", "the all-hits skeleton against itself")
+    if "launchOverheadSeconds" in res:
+        ok &= check("launchSeconds", res["launchSeconds"] * 1e6, 0.5, 20.0, "us",
+                    "back-to-back launches of a near-empty kernel")
+        ok &= check("launchOverheadSeconds", res["launchOverheadSeconds"] * 1e6, 0.0, res["launchSeconds"] * 1e6,
+                    "us", "kernel boundary on top of work, back to back: at most the empty-kernel floor")
+        ok &= check("launchIsolatedSeconds", res["launchIsolatedSeconds"] * 1e6, res["launchOverheadSeconds"] * 1e6,
+                    20.0, "us", "kernel boundary of one launch from an idle stream: at least the back-to-back one")
     ok &= check("warpsNeededToHide", res["warpsNeededToHide"], 1, 32, "waves/CU")
     # The L2s serve faster than HBM (at the loaded clock); 8 XCDs x 16 channels x
     # 128 B per cycle is the ceiling.
@@ -217,7 +224,7 @@ def hardware_json(res, spec, arch):
     # Constants of the later calibration benches, written (with the model term
     # that reads them switched on) when the log has them.
     for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec", "persistentStepCycles1",
-                 "persistentStepCycles2"] +
+                 "persistentStepCycles2", "launchSeconds", "launchOverheadSeconds", "launchIsolatedSeconds"] +
                 ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
         if key in res:
             out[key] = res[key]
@@ -228,7 +235,9 @@ def hardware_json(res, spec, arch):
         out["mallReuseModel"] = 1
     for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]), ("fillLatencyModel", ["fillLatencySec"]),
                         ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)]),
-                        ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"])):
+                        ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"]),
+                        ("launchModel", ["launchOverheadSeconds"]),
+                        ("labelModel", ["launchIsolatedSeconds", "hbmWriteBytesPerSec"])):
         if all(k in res for k in needs):
             out[term] = 1
     for key in SKELETON_KEYS:

@@ -17,7 +17,14 @@
 // what a kernel boundary costs a sequence of launches before any work (queue
 // processing, workgroup dispatch, completion signal); launchSeconds is its value
 // at 256 workgroups of 256 workitems, launchSecondsPerWorkgroup the slope of a
-// least-squares line through the 256-workitem grids.
+// least-squares line through the 256-workitem grids. A launch that carries
+// work pays less than the floor on top of it: the next launch's queue
+// processing overlaps the running kernel. So the bench also times a kernel
+// whose 256 workgroups each wait a fixed real time (5, 10, 20 and 40 us on the
+// 100 MHz counter), back to back and one launch at a time (each launch between
+// events, the stream drained before the next): launchOverheadSeconds and
+// launchIsolatedSeconds are the median of (per-launch time - wait) over the
+// waits, the time a kernel boundary adds to a launch's own work in each case.
 #include "cal_common.hpp"
 #include "gemm_mfma.hpp"
 
@@ -74,6 +81,57 @@ __global__ __launch_bounds__(Waves * 64) void readMfmaKernel(int iters, float* s
 
 __global__ __launch_bounds__(512) void launchProbeKernel(float* sink) {
     if (threadIdx.x == 0) sink[blockIdx.x] = float(blockIdx.x);
+}
+
+// Each workgroup waits `ticks` of the 100 MHz real-time counter from its own
+// start (the loop ends for every wave: the counter only advances).
+__global__ __launch_bounds__(256) void spinKernel(uint64_t ticks, float* sink) {
+    const uint64_t t0 = realtime();
+    while (realtime() - t0 < ticks) {
+    }
+    if (threadIdx.x == 0) sink[blockIdx.x] = 1.0f;
+}
+
+// Per-launch seconds of the spin kernel (256 workgroups): back to back over
+// `launches` launches, or one launch between two events with the stream
+// drained before each (isolated). Middle of kRepeats windows.
+double spinSeconds(double waitSeconds, bool isolated, float* dSink, int launches) {
+    const uint64_t ticks = uint64_t(waitSeconds * kRealtimeHz + 0.5);
+    hipEvent_t e0, e1;
+    CAL_HIP_CHECK(hipEventCreate(&e0));
+    CAL_HIP_CHECK(hipEventCreate(&e1));
+    std::vector<double> w;
+    for (int r = 0; r < kRepeats; ++r) {
+        CAL_HIP_CHECK(hipDeviceSynchronize());
+        if (isolated) {
+            std::vector<double> one;
+            for (int i = 0; i < launches; ++i) {
+                CAL_HIP_CHECK(hipDeviceSynchronize());
+                CAL_HIP_CHECK(hipEventRecord(e0, nullptr));
+                hipLaunchKernelGGL(spinKernel, dim3(256), dim3(256), 0, nullptr, ticks, dSink);
+                CAL_HIP_CHECK(hipGetLastError());
+                CAL_HIP_CHECK(hipEventRecord(e1, nullptr));
+                CAL_HIP_CHECK(hipEventSynchronize(e1));
+                float ms = 0.0f;
+                CAL_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+                one.push_back(ms * 1e-3);
+            }
+            w.push_back(middle(one));
+        } else {
+            CAL_HIP_CHECK(hipEventRecord(e0, nullptr));
+            for (int i = 0; i < launches; ++i)
+                hipLaunchKernelGGL(spinKernel, dim3(256), dim3(256), 0, nullptr, ticks, dSink);
+            CAL_HIP_CHECK(hipGetLastError());
+            CAL_HIP_CHECK(hipEventRecord(e1, nullptr));
+            CAL_HIP_CHECK(hipEventSynchronize(e1));
+            float ms = 0.0f;
+            CAL_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+            w.push_back(ms * 1e-3 / launches);
+        }
+    }
+    CAL_HIP_CHECK(hipEventDestroy(e0));
+    CAL_HIP_CHECK(hipEventDestroy(e1));
+    return middle(w);
 }
 
 // Per-launch seconds of `launches` back-to-back launches of launchProbeKernel
@@ -212,6 +270,23 @@ int main() {
     const double slope = (n * sxy - sx * sy) / (n * sxx - sx * sx);
     std::printf("CAL_RESULT launchSeconds %.6e\n", at256);
     std::printf("CAL_RESULT launchSecondsPerWorkgroup %.6e\n", slope);
+
+    // What a kernel boundary adds to a launch that carries work.
+    constexpr double kWaits[] = {5e-6, 10e-6, 20e-6, 40e-6};
+    std::vector<double> overB2b, overIso;
+    std::printf("\nkernel boundary on top of work: 256 workgroups that each wait a fixed time\n");
+    std::printf("  %9s %18s %18s\n", "wait (us)", "back to back (us)", "isolated (us)");
+    for (double wsec : kWaits) {
+        const double b2b = spinSeconds(wsec, false, dLaunchSink, 200);
+        const double iso = spinSeconds(wsec, true, dLaunchSink, 20);
+        std::printf("  %9.1f %18.3f %18.3f\n", wsec * 1e6, b2b * 1e6, iso * 1e6);
+        std::printf("CAL_INFO spinSeconds_wait%.0fus_b2b %.6e\n", wsec * 1e6, b2b);
+        std::printf("CAL_INFO spinSeconds_wait%.0fus_isolated %.6e\n", wsec * 1e6, iso);
+        overB2b.push_back(b2b - wsec);
+        overIso.push_back(iso - wsec);
+    }
+    std::printf("CAL_RESULT launchOverheadSeconds %.6e\n", middle(overB2b));
+    std::printf("CAL_RESULT launchIsolatedSeconds %.6e\n", middle(overIso));
     CAL_HIP_CHECK(hipFree(dLaunchSink));
     CAL_HIP_CHECK(hipFree(dSink));
     CAL_HIP_CHECK(hipFree(dStamps));

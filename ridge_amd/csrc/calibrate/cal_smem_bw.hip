@@ -517,19 +517,19 @@ int main() {
     CAL_HIP_CHECK(hipMalloc(&dRefill, kRefillSourceBytes));
     CAL_HIP_CHECK(hipMalloc(&dFSink, sizeof(float)));
     CAL_HIP_CHECK(hipMemcpy(dOperands, hOperands.data(), hOperands.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
-    // The refill sources hold the same U[-1,1) halves as the fragments (the
-    // 16 KiB block, tiled): the GEMM streams random operands, and the bits its
-    // loads and LDS writes toggle are part of what the loaded clock pays for.
-    auto tileRandom = [&](char* dst, size_t bytes) {
-        for (size_t off = 0; off < bytes; off += 16 * 1024)
-            CAL_HIP_CHECK(hipMemcpy(dst + off, hOperands.data(), 16 * 1024, hipMemcpyHostToDevice));
-    };
-    tileRandom(dRefill, kRefillSourceBytes);
+    // The L2-resident refill source holds the same U[-1,1) halves as the
+    // fragments (the 16 KiB block, tiled): the GEMM streams random operands, and
+    // the bits its loads and LDS writes toggle are part of what the loaded clock
+    // (mode 3 against mode 2) pays for. The L2-missing windows below keep a
+    // constant fill: they time the refill path's rate and stretch, and with
+    // random data their repeats spread by up to 25% on one box.
+    for (size_t off = 0; off < size_t(kRefillSourceBytes); off += 16 * 1024)
+        CAL_HIP_CHECK(hipMemcpy(dRefill + off, hOperands.data(), 16 * 1024, hipMemcpyHostToDevice));
     // The L2-missing windows: one per CU (workgroup g uses [g * 512 KiB, +512 KiB)).
     char* dMall = nullptr;
     const size_t mallBytes = size_t(cus) * (kMallWindowKiB << 10);
     CAL_HIP_CHECK(hipMalloc(&dMall, mallBytes));
-    tileRandom(dMall, mallBytes);
+    CAL_HIP_CHECK(hipMemset(dMall, 0x3c, mallBytes));
     constexpr int kModes = 9;
     std::vector<double> st[kModes], hz[kModes];
     for (int r = 0; r < kRepeats; ++r) {

@@ -121,6 +121,8 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("mallStretch4", h.mallStretch[4]), I("persistentStepModel", h.persistentStepModel),
         R("persistentStepCycles1", h.persistentStepCycles[0]), R("persistentStepCycles2", h.persistentStepCycles[1]),
         I("fillShareModel", h.fillShareModel), I("mallReuseModel", h.mallReuseModel), R("mallBytes", h.mallBytes),
+        I("launchModel", h.launchModel), R("launchOverheadSeconds", h.launchOverheadSeconds),
+        R("launchIsolatedSeconds", h.launchIsolatedSeconds), I("labelModel", h.labelModel),
     };
 }
 
@@ -185,6 +187,11 @@ std::string inconsistency(const HardwareModel& h) {
         return "mallReuseModel 1 reads mallRefillBytesPerSec and mallBytes, which must be positive";
     if (h.persistentStepModel == 1 && !(h.persistentStepCycles[0] > 0.0 && h.persistentStepCycles[1] > 0.0))
         return "persistentStepModel 1 reads persistentStepCycles1 and persistentStepCycles2, which must be positive";
+    if (h.launchModel == 1 && !(h.launchOverheadSeconds >= 0.0))
+        return "launchModel 1 reads launchOverheadSeconds, which must not be negative";
+    if (h.labelModel == 1 && !(h.launchIsolatedSeconds >= 0.0 && h.hbmWriteModel == 1 && h.simdsPerSM > 0))
+        return "labelModel 1 reads launchIsolatedSeconds (not negative) and needs hbmWriteModel 1 and per-SIMD "
+               "register files (simdsPerSM > 0)";
     return "";
 }
 

@@ -70,6 +70,16 @@
 //                           fill and one drain for all of them (reference: one
 //                           tile per workgroup, :91-99)
 //
+//   kernel boundary       = hw.launchModel 1: each launch of a back-to-back
+//                           sequence pays launchOverheadSeconds on top of its
+//                           work (reference: launches cost their work alone)
+//   label                 = hw.labelModel 1: the model predicts what the
+//                           counters read on one launch from an idle stream
+//                           (DRAM share, body share from a second K, CU share,
+//                           MFMA and LDS busy shares) and labels that prediction
+//                           with the counters' decision table (reference: the
+//                           derating furthest from 1, :129-143)
+//
 // With the defaults (a100() or a reference JSON) every term reduces to the
 // reference's expression in the same double-precision operation order, so the
 // A100 predictions match the reference bit for bit; integer divisions are kept
@@ -113,6 +123,16 @@ namespace {
 
 // Loader wavefronts of a persistent workgroup (the kernels' PersistentTraits).
 constexpr int kPersistentLoaderWaves = 2;
+
+// The counters' decision table (the rocprofv3 label check, registration 3),
+// first match wins; labelModel 1 applies it to the model's own prediction of
+// those counters.
+constexpr double kDramShareMin = 0.70;       // DRAM share >= 0.70                      -> HBM
+constexpr double kCuShareMin = 0.55;         // CU share < 0.55                         -> WAVES
+constexpr double kBodyShareMin = 0.60;       // body share < 0.60                       -> ENVELOPE
+constexpr double kLdsOverMfmaMin = 0.70;     // LDS share >= 0.70 x MFMA share          -> SMEM
+constexpr double kMfmaOverBodyMin = 0.60;    // MFMA share / min(1, body share) >= 0.60 -> TENSOR_CORE
+                                             // otherwise                               -> OCC
 
 // LDS of a persistent workgroup's epilogue staging: each compute wave stages
 // the largest number of 16-row tile-rows that divides its tile-rows and fits
@@ -228,7 +248,7 @@ double persistentStepRatio(const GemmConfig& cfg, const HardwareModel& hw, int d
 
 }  // namespace
 
-Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
+Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
     GemmConfig cfg = cfgIn;
     const MmaShape mma = mmaShapeFor(cfg.dtype, hw);
     if (cfg.mmaM == 0) {
@@ -493,6 +513,8 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         const double flops = 2.0 * M * N * K;
         const double readBytes = std::max(flops / panelIntensity, (M * K + K * N) * db);
         const double writeBytes = M * N * hw.cBytes;
+        p.dramReadBytes = readBytes;
+        p.dramWriteBytes = writeBytes;
         double seconds = readBytes / hw.hbmBytesPerSec + writeBytes / hw.hbmWriteBytesPerSec;
         if (hw.mallReuseModel == 1 && (M * K + K * N) * db <= hw.mallBytes) {
             // A and B stay in the MALL: HBM supplies each byte once, and the
@@ -537,6 +559,16 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         p.fillRounds = rounds;
         p.predictedTFLOPS = std::min(computeTFLOPS, p.hbmTFLOPS);
     }
+    if (hw.launchModel == 1) {
+        // A kernel boundary in a back-to-back sequence: the next launch's queue
+        // processing overlaps the running kernel, the rest of the boundary adds
+        // to whichever ceiling binds.
+        const double flops = 2.0 * double(cfg.M) * double(cfg.N) * double(cfg.K);
+        computeTFLOPS = flops / (flops / (computeTFLOPS * 1e12) + hw.launchOverheadSeconds) / 1e12;
+        p.hbmTFLOPS = flops / (flops / (p.hbmTFLOPS * 1e12) + hw.launchOverheadSeconds) / 1e12;
+        p.computeTFLOPS = computeTFLOPS;
+        p.predictedTFLOPS = std::min(computeTFLOPS, p.hbmTFLOPS);
+    }
     if (p.hbmTFLOPS < computeTFLOPS) {
         p.bottleneck = Bottleneck::Hbm;
     } else {
@@ -553,6 +585,78 @@ Prediction predict(const GemmConfig& cfgIn, const HardwareModel& hw) {
         else
             p.bottleneck = Bottleneck::Occupancy;
     }
+    return p;
+}
+
+namespace {
+
+// labelModel 1: what the counters read on one launch of cfg from an idle
+// stream, and the decision table's label for it.
+void observe(const GemmConfig& cfg, const HardwareModel& hw, Prediction& p) {
+    const double M = double(cfg.M), N = double(cfg.N);
+    const double flops = 2.0 * M * N * double(cfg.K);
+    const double backToBack = hw.launchModel == 1 ? hw.launchOverheadSeconds : 0.0;
+    // One launch from an idle stream: the predicted work plus that launch's
+    // kernel boundary in place of the back-to-back one.
+    auto isolated = [&](const Prediction& q, double fl) {
+        return fl / (q.predictedTFLOPS * 1e12) - backToBack + hw.launchIsolatedSeconds;
+    };
+    p.kernelSeconds = isolated(p, flops);
+    p.dramShare = (p.dramReadBytes / hw.hbmBytesPerSec + p.dramWriteBytes / hw.hbmWriteBytesPerSec) / p.kernelSeconds;
+
+    // Body share: the share of the duration that scales with K, from the
+    // duration at a second K (K / 2 when that is a whole number of K tiles,
+    // else 2 K): t(K) = fixed + body, t(f K) = fixed + f body.
+    const long long half = cfg.K / 2;
+    const bool useHalf = cfg.K % 2 == 0 && cfg.BK > 0 && half % cfg.BK == 0 && half >= cfg.BK;
+    GemmConfig other = cfg;
+    other.K = useHalf ? half : 2 * cfg.K;
+    p.bodyFactor = useHalf ? 0.5 : 2.0;
+    const Prediction q = predictCore(other, hw);
+    const double t2 = isolated(q, 2.0 * M * N * double(other.K));
+    p.bodyShare = (t2 - p.kernelSeconds) / ((p.bodyFactor - 1.0) * p.kernelSeconds);
+
+    // CU share: a persistent grid holds min(tiles, slots) workgroups for the
+    // whole launch; a one-tile-per-workgroup grid runs ceil(tiles / slots)
+    // rounds, all CUs busy but in the last, which keeps min(1, tail / CUs).
+    const double cus = double(hw.numSMs);
+    const bool persistent = hw.persistentModel == 1 && cfg.schedule == 2;
+    if (persistent) {
+        p.cuShare = std::min(1.0, std::min(p.totalCtas, p.ctaSlots) / cus);
+    } else {
+        const double rounds = std::ceil(p.totalCtas / p.ctaSlots);
+        const double tail = p.totalCtas - (rounds - 1.0) * p.ctaSlots;
+        p.cuShare = ((rounds - 1.0) + std::min(1.0, tail / cus)) / rounds;
+    }
+
+    // Busy shares at the model's loaded clock: every MFMA costs its issue
+    // cycles on one SIMD, every K-step its fragment reads on the CU's LDS.
+    const MmaShape mma = mmaShapeFor(cfg.dtype, hw);
+    const double clock = hw.clockHz * p.powerClockFactor;
+    const double simds = cus * hw.simdsPerSM;
+    const double mfmaCyclesPerSimd = flops / double(mma.flops) * hw.mmaCyclesPerInst * hw.simdsPerSM / simds;
+    p.mfmaShare = mfmaCyclesPerSimd / (p.kernelSeconds * clock);
+    p.ldsShare = p.totalCtas * p.kSteps * p.tSmemCycles / cus / (p.kernelSeconds * clock);
+
+    if (p.dramShare >= kDramShareMin)
+        p.bottleneck = Bottleneck::Hbm;
+    else if (p.cuShare < kCuShareMin)
+        p.bottleneck = Bottleneck::Waves;
+    else if (p.bodyShare < kBodyShareMin)
+        p.bottleneck = Bottleneck::Envelope;
+    else if (p.ldsShare >= kLdsOverMfmaMin * p.mfmaShare)
+        p.bottleneck = Bottleneck::Smem;
+    else if (p.mfmaShare / std::min(1.0, p.bodyShare) >= kMfmaOverBodyMin)
+        p.bottleneck = Bottleneck::TensorCore;
+    else
+        p.bottleneck = Bottleneck::Occupancy;
+}
+
+}  // namespace
+
+Prediction predict(const GemmConfig& cfg, const HardwareModel& hw) {
+    Prediction p = predictCore(cfg, hw);
+    if (hw.labelModel == 1 && p.bottleneck != Bottleneck::DoesNotFit) observe(cfg, hw, p);
     return p;
 }
 

@@ -133,6 +133,15 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     out->refillMissShare = p.refillMissShare;
     out->mallLoad = p.mallLoad;
     out->mallStretch = p.mallStretch;
+    out->kernelSeconds = p.kernelSeconds;
+    out->dramReadBytes = p.dramReadBytes;
+    out->dramWriteBytes = p.dramWriteBytes;
+    out->dramShare = p.dramShare;
+    out->bodyFactor = p.bodyFactor;
+    out->bodyShare = p.bodyShare;
+    out->cuShare = p.cuShare;
+    out->mfmaShare = p.mfmaShare;
+    out->ldsShare = p.ldsShare;
     return 0;
 }
 

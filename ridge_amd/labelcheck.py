@@ -83,9 +83,18 @@ def design_factors(c):
     return [1] + ([0.5] if c["K"] % 2 == 0 and half % c["BK"] == 0 and half >= c["BK"] else []) + [2]
 
 
+def body_factors(c):
+    """Registration 3: the second K of the body share, K / 2 when that is a whole
+    number of K tiles (at least one), else K x 2; the model's labelModel 1 uses
+    the same rule (Prediction.bodyFactor)."""
+    half = c["K"] // 2
+    return [1, 0.5] if c["K"] % 2 == 0 and half % c["BK"] == 0 and half >= c["BK"] else [1, 2]
+
+
 REGISTRATIONS = {1: Registration(1, "rocprof-label", 0), 2: Registration(2, "rocprof-label2", 16),
+                 3: Registration(3, "rocprof-label3", factors=body_factors),
                  "design": Registration("design", "rocprof-label-design", factors=design_factors)}
-CURRENT = 2
+CURRENT = 3
 # Registration 1's files under their original names (kept for its tests).
 HW_JSON = REGISTRATIONS[1].hw_json
 SOURCES = REGISTRATIONS[1].sources
@@ -157,6 +166,76 @@ REQUIRED_2 = [
     ((16384, 128, 8192, 128, 64, 64, 64, 32, 6, 8), "persistent row, tall-skinny"),
 ]
 CONTROL_2 = REQUIRED_2[0][0]
+
+# Registration 3 (data/sweep/rocprof-label3-mapping.md): configs drawn from the
+# fifth held-out sweep's cross product (registered, not yet measured) plus the
+# BASELINE configs' best rows.
+HELDOUT5_SHAPES = os.path.join(SWEEP_DIR, "mi355x-heldout5-registered.csv")
+TABLE3 = os.path.join(SWEEP_DIR, "rocprof-label3-table.csv")
+LABEL_ORDER_3 = ["HBM", "WAVES", "ENVELOPE", "SMEM", "TENSOR_CORE", "OCC"]
+REQUIRED_3 = [
+    ((4096, 4096, 4096, 256, 256, 32, 128, 64, 3, 4), "baseline-4096cube-headline", "control: the headline row"),
+    ((1024, 1024, 1024, 64, 64, 64, 32, 32, 4, 8), "baseline-1024cube", "required: BASELINE config, best row"),
+    ((8192, 8192, 128, 256, 128, 32, 64, 64, 6, 4), "baseline-small-k", "required: BASELINE config, best row"),
+    ((16384, 128, 8192, 64, 128, 128, 32, 64, 3, 8), "baseline-tall-skinny", "required: BASELINE config, best row"),
+]
+TABLE3_COLUMNS = KEY_FIELDS + ["persistent", "regsPerThread", "schedule"]
+
+
+def write_table3(path=TABLE3):
+    """The kernel table at registration time with each row's register count and
+    schedule (from the built library), so the selection re-derives without it."""
+    from ridge_amd import gemm as G
+    rows = [dict(BM=v.BM, BN=v.BN, BK=v.BK, WM=v.WM, WN=v.WN, stages=v.stages, groupM=v.groupM,
+                 persistent=int(v.schedule == 2), regsPerThread=v.regsPerThread, schedule=v.schedule)
+            for v in G.variants()]
+    T.write(path, TABLE3_COLUMNS, rows, ["the kernel table registration 3 is selected from (ridge_amd/csrc/"
+                                         "gemm_variants.def and the compiler's register counts at registration)"])
+
+
+def select_configs3(reg):
+    """Registration 3's rule. Every shape of the fifth held-out sweep times every
+    row of the frozen table is labelled by the frozen model; within each label
+    (in LABEL_ORDER_3) the configs are sorted by (tag, BM, BN, BK, WM, WN, stages,
+    groupM) and the first PER_LABEL of distinct shapes are taken. The control and
+    the BASELINE configs' best rows (REQUIRED_3) come first."""
+    hw = RM.Hardware(reg.hw_json)
+    table = [{k: int(v) for k, v in r.items()} for r in _read_rows(TABLE3)]
+    by_key = {tuple(t[k] for k in KEY_FIELDS): t for t in table}
+
+    def config(M, N, K, t, tag):
+        r = {"M": M, "N": N, "K": K, "tag": tag, "regsPerThread": t["regsPerThread"], "schedule": t["schedule"],
+             **{k: t[k] for k in KEY_FIELDS}}
+        p = predict_row(hw, r, True)
+        return r, p
+
+    def row(label, r, p, why):
+        return {"predicted_label": label, "model_label": p["bottleneck"], "tag": r["tag"], "M": r["M"], "N": r["N"],
+                "K": r["K"], **{k: r[k] for k in KEY_FIELDS}, "regsPerThread": r["regsPerThread"],
+                "theoretical_waves_per_cu": p["ctasPerSM"] * p["numWarps"],
+                "pred_tflops": round(p["predictedTFLOPS"], 3), "measured_tflops": "", "schedule": r["schedule"],
+                "why": why}
+
+    out = []
+    for key, tag, why in REQUIRED_3:
+        r, p = config(key[0], key[1], key[2], by_key[key[3:]], tag)
+        out.append(row("CONTROL" if why.startswith("control") else p["bottleneck"], r, p, why))
+    groups = {}
+    for M, N, K, tag in T.read_shapes(HELDOUT5_SHAPES):
+        for t in table:
+            r, p = config(M, N, K, t, tag)
+            groups.setdefault(p["bottleneck"], []).append((r, p))
+    for label in LABEL_ORDER_3:
+        shapes = set()
+        for r, p in sorted(groups.get(label, []), key=lambda rp: (rp[0]["tag"],) + tuple(rp[0][k] for k in KEY_FIELDS)):
+            shape = (r["M"], r["N"], r["K"])
+            if shape in shapes:
+                continue
+            shapes.add(shape)
+            out.append(row(label, r, p, "per-label rule"))
+            if len(shapes) == PER_LABEL:
+                break
+    return out
 
 
 def select_configs(sources=SOURCES, hw_json=HW_JSON, per_label=PER_LABEL, registration=1):
@@ -260,6 +339,9 @@ def cmd_select(args):
     if reg.number == "design":
         rows = design_configs()
         note = "label-design set (in-sample, never scored); see ridge_amd/labelcheck.py design_configs"
+    elif reg.number == 3:
+        rows = select_configs3(reg)
+        note = "registered before any rocprofv3 run; see %s" % os.path.relpath(reg.mapping, ROOT)
     else:
         rows = select_configs(reg.sources, reg.hw_json, registration=reg.number)
         note = "registered before any rocprofv3 run; see %s" % os.path.relpath(reg.mapping, ROOT)
@@ -367,7 +449,9 @@ def _counter(dispatch, name, xcds, grbm):
 def cmd_gather(args):
     reg = REGISTRATIONS[args.registration]
     configs = load_configs(args.configs or reg.configs)
-    with open(reg.hw_json) as f:
+    # The design set has no frozen calibration: the XCD count is the chip's.
+    hw_json = reg.hw_json if os.path.exists(reg.hw_json) else os.path.join(ROOT, "data", "hardware", "mi355x.json")
+    with open(hw_json) as f:
         hwj = json.load(f)
     xcds = int(hwj.get("numXcds", 8))
     facs = [reg.factors(c) for c in configs]
@@ -474,6 +558,59 @@ def counter_label2(d):
     return "UNDECIDED"
 
 
+# Registration 3's decision table (data/sweep/rocprof-label3-mapping.md section 3),
+# first match wins. The model's labelModel 1 applies the same table to its own
+# prediction of these quantities.
+DRAM_SHARE_MIN_3 = 0.70      # rule 1: DRAM share >= 0.70                        -> HBM
+CU_SHARE_MIN_3 = 0.55        # rule 2: CU share < 0.55                           -> WAVES
+BODY_SHARE_MIN_3 = 0.60      # rule 3: body share < 0.60                         -> ENVELOPE
+LDS_OVER_MFMA_MIN_3 = 0.70   # rule 4: LDS share >= 0.70 x MFMA share            -> SMEM
+MFMA_OVER_BODY_MIN_3 = 0.60  # rule 5: MFMA share / min(1, body share) >= 0.60   -> TENSOR_CORE
+                             # rule 6: otherwise                                 -> OCC
+CONTROL_CU_SHARE_3 = (0.70, 1.05)
+
+
+def derived3(row, hwj):
+    """Registration 3's quantities, each over the kernel-trace duration of the
+    launch at K, none over the counters' own collection window (which runs several
+    microseconds past a short kernel): the SQ cycle counts are converted at the
+    launch's clock, its GRBM cycles over its duration, capped at the engine's
+    nominal clock. The body share comes from the duration at the second K of
+    body_factors."""
+    cus = float(hwj["numSMs"])
+    simds = cus * float(hwj.get("simdsPerSM", 4))
+    dur = float(row["duration_ns"]) * 1e-9
+    clock = min(float(row["GRBM_GUI_ACTIVE"]) / dur, float(hwj["nominalClockHz"]))
+    read = float(row["FETCH_SIZE"]) * FETCH_SCALE * 1024.0
+    write = float(row["WRITE_SIZE"]) * WRITE_SCALE * 1024.0
+    d = {"clock_hz": clock, "duration_us": dur * 1e6}
+    d["dram_share"] = (read / float(hwj["hbmBytesPerSec"]) + write / float(hwj["hbmWriteBytesPerSec"])) / dur
+    d["mfma_share"] = float(row["SQ_VALU_MFMA_BUSY_CYCLES"]) / (simds * dur * clock)
+    d["lds_share"] = float(row["SQ_LDS_IDX_ACTIVE"]) / (cus * dur * clock)
+    d["cu_share"] = float(row["SQ_BUSY_CU_CYCLES"]) / (cus * dur * clock)
+    f = body_factors({"K": int(row["K"]), "BK": int(row["BK"])})[1]
+    t2 = float(row[REGISTRATIONS[3].duration_column(f)]) * 1e-9
+    d["body_factor"] = f
+    d["body_share"] = (t2 - dur) / ((f - 1.0) * dur)
+    return d
+
+
+def counter_label3(d):
+    """Registration 3's table, first match wins. Also applied, in a test, to the
+    model's predicted quantities, which must give the model's own label."""
+    if d["dram_share"] >= DRAM_SHARE_MIN_3:
+        return "HBM"
+    if d["cu_share"] < CU_SHARE_MIN_3:
+        return "WAVES"
+    if d["body_share"] < BODY_SHARE_MIN_3:
+        return "ENVELOPE"
+    if d["lds_share"] >= LDS_OVER_MFMA_MIN_3 * d["mfma_share"]:
+        return "SMEM"
+    if d["mfma_share"] / min(1.0, d["body_share"]) >= MFMA_OVER_BODY_MIN_3:
+        return "TENSOR_CORE"
+    return "OCC"
+
+
 def score(rows, hwj, registration=1):
     """(results, agree, need, control_ok): results over every row, the count of
     scored rows (the control excluded) whose counter label equals the model's,
@@ -483,6 +620,13 @@ def score(rows, hwj, registration=1):
     control_ok = True
     reg = REGISTRATIONS[registration]
     for r in rows:
+        if registration == 3:
+            d = derived3(r, hwj)
+            results.append((r, d, counter_label3(d)))
+            if r["predicted_label"] == "CONTROL":
+                lo, hi = CONTROL_CU_SHARE_3
+                control_ok = control_ok and lo <= d["cu_share"] <= hi
+            continue
         if registration == 2:
             d = derived2(r, hwj, reg.long_factor)
             results.append((r, d, counter_label2(d)))
@@ -498,12 +642,43 @@ def score(rows, hwj, registration=1):
     return results, agree, need, control_ok
 
 
+def _print_score3(results, agree, need, control_ok):
+    print("%-11s %-20s %-26s %8s %5s %5s %5s %5s %5s %5s  %-11s" % (
+        "model", "shape", "variant", "us", "DRAM", "CU", "body", "LDS", "MFMA", "GHz", "counters"))
+    by_label = {}
+    for r, d, lab in results:
+        shape = "%sx%sx%s" % (r["M"], r["N"], r["K"])
+        var = "%sx%sx%s w%sx%s s%s g%s" % tuple(r[k] for k in KEY_FIELDS)
+        verdict = "" if r["predicted_label"] == "CONTROL" else (
+            "agree" if lab == r["predicted_label"] else "DISAGREE")
+        print("%-11s %-20s %-26s %8.1f %5.2f %5.2f %5.2f %5.2f %5.2f %5.2f  %-11s %s" % (
+            r["predicted_label"], shape, var, d["duration_us"], d["dram_share"], d["cu_share"], d["body_share"],
+            d["lds_share"], d["mfma_share"], d["clock_hz"] / 1e9, lab, verdict))
+        if r["predicted_label"] != "CONTROL":
+            s = by_label.setdefault(r["predicted_label"], [0, 0])
+            s[0] += lab == r["predicted_label"]
+            s[1] += 1
+    print()
+    for lab in LABEL_ORDER_3:
+        if lab in by_label:
+            print("  %-11s %d of %d agree" % (lab, by_label[lab][0], by_label[lab][1]))
+    if not control_ok:
+        print("\ncontrol CU share outside [%g, %g]: the normalisations are wrong, the run is VOID" % CONTROL_CU_SHARE_3)
+        return 2
+    scored = sum(1 for r, d, lab in results if r["predicted_label"] != "CONTROL")
+    verdict = "PASS" if agree >= need else "FAIL"
+    print("\n%d of %d configs agree (registered pass: >= %d) -> %s" % (agree, scored, need, verdict))
+    return 0 if verdict == "PASS" else 1
+
+
 def cmd_score(args):
     reg = REGISTRATIONS[args.registration]
     with open(reg.hw_json) as f:
         hwj = json.load(f)
     rows = _read_rows(args.counters_csv or reg.counters)
     results, agree, need, control_ok = score(rows, hwj, reg.number)
+    if reg.number == 3:
+        return _print_score3(results, agree, need, control_ok)
     print("%-9s %-28s %-22s %6s %6s %6s %6s %6s %6s %6s  %-9s" % (
         "model", "shape", "variant", "HBM%", "SIMD%", "occ%", "theo%", "LDS%", "MFMA%", "steady", "counters"))
     by_label = {}

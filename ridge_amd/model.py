@@ -33,7 +33,9 @@ _PRED_FIELDS = [("predictedTFLOPS", ctypes.c_double), ("bottleneck", ctypes.c_in
     [("numWarps", ctypes.c_int), ("ctasPerSM", ctypes.c_int)] + \
     [(n, ctypes.c_double) for n in ("tComputeCycles", "tSmemCycles", "tStepCycles", "reuseTilesM", "reuseTilesN",
                                     "compulsoryIntensity", "tailClockFactor", "l2HitBytes", "powerClockFactor",
-                                    "fillRounds", "refillMissShare", "mallLoad", "mallStretch")]
+                                    "fillRounds", "refillMissShare", "mallLoad", "mallStretch",
+                                    "kernelSeconds", "dramReadBytes", "dramWriteBytes", "dramShare", "bodyFactor",
+                                    "bodyShare", "cuShare", "mfmaShare", "ldsShare")]
 
 
 class _Prediction(ctypes.Structure):

@@ -151,7 +151,10 @@ def test_binding_struct_layouts_match_the_libraries():
     L = RM.lib()
     assert L.ridge_model_config_size() == ctypes.sizeof(RM._Config)
     assert L.ridge_model_prediction_size() == ctypes.sizeof(RM._Prediction)
-    # The prediction ends with the gfx950 fields, after the reference's.
-    assert [f for f, _ in RM._Prediction._fields_][-7:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor",
-                                                            "fillRounds", "refillMissShare", "mallLoad",
-                                                            "mallStretch"]
+    # The prediction ends with the gfx950 fields, after the reference's, and the
+    # counter observables last.
+    assert [f for f, _ in RM._Prediction._fields_][-16:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor",
+                                                             "fillRounds", "refillMissShare", "mallLoad",
+                                                             "mallStretch", "kernelSeconds", "dramReadBytes",
+                                                             "dramWriteBytes", "dramShare", "bodyFactor",
+                                                             "bodyShare", "cuShare", "mfmaShare", "ldsShare"]

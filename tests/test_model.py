@@ -29,6 +29,11 @@ def mi355x():
     return RM.Hardware("mi355x")
 
 
+@pytest.fixture(scope="module")
+def mi355x_calibrated():
+    return RM.Hardware(os.path.join(ROOT, "data", "hardware", "mi355x.json"))
+
+
 def test_a100_worked_example(a100):
     # test-model.cpp:47-101, values derived by hand there.
     p = RM.predict(a100, M=4096, N=4096, K=4096, BM=128, BN=128, BK=32, warpM=64, warpN=64, stages=3,
@@ -741,3 +746,97 @@ def test_fill_share_model_fetches_each_panel_slice_once_per_xcd(tmp_path):
     bad.write_text(_CDNA4_JSON % ', "fillShareModel": 1')
     with pytest.raises(ValueError, match="fillShareModel 1"):
         RM.Hardware(str(bad))
+
+
+def test_launch_model_adds_the_kernel_boundary_to_each_launch(tmp_path):
+    """launchModel 1 with launchOverheadSeconds 2 us: each launch's time grows by
+    2 us on both ceilings (a uniform and a persistent row), so the prediction is
+    flops / (flops / before + 2 us); a negative overhead is refused."""
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % "")
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % ', "launchModel": 1, "launchOverheadSeconds": 2e-6')
+    hw_off, hw_on = RM.Hardware(str(off)), RM.Hardware(str(on))
+    for cfg in (dict(M=4096, N=4096, K=1024, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128),
+                dict(M=8192, N=8192, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=4, regsPerThread=185,
+                     schedule=2)):
+        a, b = RM.predict(hw_off, **cfg), RM.predict(hw_on, **cfg)
+        flops = 2.0 * cfg["M"] * cfg["N"] * cfg["K"]
+        for key in ("predictedTFLOPS", "computeTFLOPS", "hbmTFLOPS"):
+            assert b[key] == pytest.approx(flops / (flops / (a[key] * 1e12) + 2e-6) / 1e12)
+        assert b["bottleneck"] == a["bottleneck"]
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "launchModel": 1, "launchOverheadSeconds": -1e-6')
+    with pytest.raises(ValueError, match="launchModel 1"):
+        RM.Hardware(str(bad))
+
+
+_LABEL_JSON = (', "hbmWriteModel": 1, "hbmWriteBytesPerSec": 5e12, "simdsPerSM": 4, "regsPerSimdLane": 512, '
+               '"labelModel": 1, "launchIsolatedSeconds": 3e-6')
+
+
+def test_label_model_predicts_the_counters_of_one_launch(tmp_path):
+    """labelModel 1 on the placeholders (2.4 GHz, 4 cycles per MFMA per CU, HBM
+    reads at 8 TB/s, writes at 5 TB/s, one launch from an idle stream costs its
+    work plus 3 us):
+      duration    = flops / predicted + 3 us;
+      DRAM share  = (L2-missed A/B bytes / 8e12 + C bytes / 5e12) / duration;
+      MFMA share  = MFMAs (flops / 16384) x 16 cycles / 1024 SIMDs / (duration x 2.4 GHz);
+      LDS share   = tiles x K-steps x fragment-read cycles / 256 CUs / (duration x 2.4 GHz);
+      body share  = (t(K / 2) - t(K)) / (-t(K) / 2) at K = 4096 (K / 2 holds whole
+                    K tiles), from K x 2 at K = 128 on a BK = 128 row (K / 2 does not);
+      CU share    = 64 tiles of 128x128 at 1024 x 1024, one round: 64 / 256 = 0.25
+                    (and the grid is labelled WAVES, its DRAM share being small)."""
+    f = tmp_path / "lab.json"
+    f.write_text(_CDNA4_JSON % _LABEL_JSON)
+    hw = RM.Hardware(str(f))
+    cfg = dict(M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=3, regsPerThread=200,
+               groupM=4, schedule=1)
+    p = RM.predict(hw, **cfg)
+    flops = 2.0 * 4096 ** 3
+    t = flops / (p["predictedTFLOPS"] * 1e12) + 3e-6
+    assert p["kernelSeconds"] == pytest.approx(t)
+    assert p["dramWriteBytes"] == 4096 * 4096 * 2
+    assert p["dramShare"] == pytest.approx((p["dramReadBytes"] / 8e12 + p["dramWriteBytes"] / 5e12) / t)
+    assert p["mfmaShare"] == pytest.approx(flops / 16384 * 16 / 1024 / (t * 2.4e9))
+    assert p["ldsShare"] == pytest.approx(p["totalCtas"] * p["kSteps"] * p["tSmemCycles"] / 256 / (t * 2.4e9))
+    half = RM.predict(hw, **dict(cfg, K=2048))
+    t_half = 2.0 * 4096 * 4096 * 2048 / (half["predictedTFLOPS"] * 1e12) + 3e-6
+    assert p["bodyFactor"] == 0.5
+    assert p["bodyShare"] == pytest.approx((t_half - t) / (-0.5 * t))
+    k128 = dict(M=8192, N=8192, K=128, BM=128, BN=64, BK=128, warpM=64, warpN=32, stages=3, regsPerThread=131,
+                groupM=8, schedule=2)
+    q = RM.predict(hw, **k128)
+    q2 = RM.predict(hw, **dict(k128, K=256))
+    tq = 2.0 * 8192 * 8192 * 128 / (q["predictedTFLOPS"] * 1e12) + 3e-6
+    tq2 = 2.0 * 8192 * 8192 * 256 / (q2["predictedTFLOPS"] * 1e12) + 3e-6
+    assert q["bodyFactor"] == 2.0
+    assert q["bodyShare"] == pytest.approx((tq2 - tq) / tq)
+    small = RM.predict(hw, M=1024, N=1024, K=4096, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2,
+                       regsPerThread=128)
+    assert small["cuShare"] == pytest.approx(0.25)
+    assert small["dramShare"] < 0.70 and small["bottleneck"] == "WAVES"
+    # The reference's label without the switch.
+    plain = tmp_path / "plain.json"
+    plain.write_text(_CDNA4_JSON % _LABEL_JSON.replace('"labelModel": 1', '"labelModel": 0'))
+    p0 = RM.predict(RM.Hardware(str(plain)), **cfg)
+    assert p0["kernelSeconds"] == 0.0 and p0["predictedTFLOPS"] == p["predictedTFLOPS"]
+
+
+def test_label_model_is_the_registered_counter_table(mi355x_calibrated):
+    """With the committed calibration, the model's label is the label check's
+    registered decision table (ridge_amd.labelcheck.counter_label3) applied to the
+    model's own predicted counters, on every row of the in-sample sweep, the
+    fourth held-out sweep and the BASELINE configs; the first rule that matches
+    decides, so a table in another order or with other thresholds disagrees."""
+    from ridge_amd import labelcheck as LC
+    from ridge_amd import tables as T
+    seen = set()
+    for name in ("mi355x.csv", "mi355x-heldout4.csv", "mi355x-baseline-configs.csv"):
+        for r in T.read(os.path.join(ROOT, "data", "measured", name)).records:
+            p = LC.predict_row(mi355x_calibrated, r, True)
+            obs = {"dram_share": p["dramShare"], "cu_share": p["cuShare"], "body_share": p["bodyShare"],
+                   "lds_share": p["ldsShare"], "mfma_share": p["mfmaShare"]}
+            assert LC.counter_label3(obs) == p["bottleneck"], r
+            seen.add(p["bottleneck"])
+    assert {"HBM", "WAVES", "ENVELOPE", "SMEM", "TENSOR_CORE"} <= seen
