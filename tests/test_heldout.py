@@ -231,3 +231,28 @@ def test_fourth_heldout_replicate_on_another_box():
         return {tag: v[1] for tag, v in out.items()}
     a, b = best(MEASURED4), best(rep)
     assert sum(a[t] == b[t] for t in a) == 13
+
+
+# The fifth held-out sweep (data/sweep/mi355x-heldout5.md): the model with the
+# kernel-boundary and counter-label terms, frozen before measuring.
+REGISTERED5 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout5-registered.csv")
+FROZEN5 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout5-hw.json")
+TABLE5 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout5-table.csv")
+
+
+def test_fifth_heldout_registration():
+    """14 shapes none of the earlier sets or the BASELINE configs hold, against the
+    fourth set's 24-row table; the frozen constants switch on the boundary and
+    label terms."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED5)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    assert len(held) == 14 and not held & earlier
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE5) == keys(TABLE4) and len(set(keys(TABLE5))) == 24
+    with open(FROZEN5) as f:
+        fifth = json.load(f)
+    assert fifth["launchModel"] == 1 and fifth["labelModel"] == 1

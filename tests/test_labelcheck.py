@@ -221,3 +221,93 @@ def test_registration_2_counters_score_as_reported():
             s[0] += lab == r["predicted_label"]
             s[1] += 1
     assert split == {"SMEM": [0, 4], "WAVES": [3, 4], "ENVELOPE": [2, 5], "HBM": [3, 8]}
+
+
+REG3 = LC.REGISTRATIONS[3]
+
+
+def test_registration_3_configs_are_its_selection(tmp_path):
+    """Registration 3's committed config list re-derives from its frozen files
+    (the fifth held-out sweep's shapes, the frozen table and calibration): the
+    control, the three BASELINE rows, then at most four configs of distinct
+    shapes per label in the registered order, every one labelled so by the model."""
+    out = tmp_path / "c3.csv"
+    LC.main(["--registration", "3", "select", "--out", str(out)])
+    now = LC._read_rows(str(out))
+    committed = LC._read_rows(REG3.configs)
+    assert now == committed
+    rows = LC.load_configs(REG3.configs)
+    assert rows[0]["predicted_label"] == "CONTROL"
+    assert [r["why"] for r in rows[1:4]] == ["required: BASELINE config, best row"] * 3
+    fresh = rows[4:]
+    labels = [r["predicted_label"] for r in fresh]
+    assert [LC.LABEL_ORDER_3.index(x) for x in labels] == sorted(LC.LABEL_ORDER_3.index(x) for x in labels)
+    for lab in set(labels):
+        shapes = [(r["M"], r["N"], r["K"]) for r in fresh if r["predicted_label"] == lab]
+        assert len(shapes) == len(set(shapes)) <= LC.PER_LABEL
+    assert all(r["model_label"] == r["predicted_label"] for r in rows[1:])
+    heldout = {(m, n, k) for m, n, k, _ in LC.T.read_shapes(LC.HELDOUT5_SHAPES)}
+    assert all((r["M"], r["N"], r["K"]) in heldout for r in fresh)
+    assert len(rows) - 1 == 26
+
+
+def test_registration_3_body_factor_rule():
+    assert LC.body_factors({"K": 4096, "BK": 32}) == [1, 0.5]
+    assert LC.body_factors({"K": 128, "BK": 64}) == [1, 0.5]     # one K tile at K / 2
+    assert LC.body_factors({"K": 128, "BK": 128}) == [1, 2]      # K / 2 is half a tile
+    assert LC.body_factors({"K": 192, "BK": 64}) == [1, 2]       # 96 is not a whole tile
+
+
+def _d3(**kw):
+    base = dict(dram_share=0.3, cu_share=0.9, body_share=0.9, lds_share=0.2, mfma_share=0.7)
+    base.update(kw)
+    return base
+
+
+def test_registration_3_decision_table():
+    assert LC.counter_label3(_d3()) == "TENSOR_CORE"
+    assert LC.counter_label3(_d3(dram_share=0.70, cu_share=0.1, body_share=0.1)) == "HBM"
+    assert LC.counter_label3(_d3(cu_share=0.549, body_share=0.1)) == "WAVES"   # WAVES before ENVELOPE
+    assert LC.counter_label3(_d3(cu_share=0.55, body_share=0.599)) == "ENVELOPE"
+    assert LC.counter_label3(_d3(lds_share=0.49)) == "SMEM"                     # 0.49 >= 0.7 x 0.7
+    assert LC.counter_label3(_d3(lds_share=0.48)) == "TENSOR_CORE"
+    # MFMA share over the body share (capped at 1): 0.48 / 0.8 = 0.6.
+    assert LC.counter_label3(_d3(mfma_share=0.48, body_share=0.8, lds_share=0.1)) == "TENSOR_CORE"
+    assert LC.counter_label3(_d3(mfma_share=0.47, body_share=0.8, lds_share=0.1)) == "OCC"
+    assert LC.counter_label3(_d3(mfma_share=0.59, body_share=1.3, lds_share=0.1)) == "OCC"
+
+
+def test_registration_3_derived_quantities():
+    """Shares over the kernel-trace duration at the launch's clock (GRBM cycles
+    over the duration, capped at the nominal clock), and the two-point body share."""
+    hwj = {"numSMs": 256, "simdsPerSM": 4, "hbmBytesPerSec": 8e12, "hbmWriteBytesPerSec": 4e12,
+           "nominalClockHz": 2.4e9}
+    row = {"K": 4096, "BK": 32, "duration_ns": 100000.0, "duration_x0.5_ns": 55000.0,
+           "GRBM_GUI_ACTIVE": 180000.0, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 90000.0,
+           "SQ_LDS_IDX_ACTIVE": 256 * 36000.0, "SQ_BUSY_CU_CYCLES": 256 * 162000.0,
+           "FETCH_SIZE": 100000.0, "WRITE_SIZE": 50000.0}
+    d = LC.derived3(row, hwj)
+    assert d["clock_hz"] == pytest.approx(1.8e9)                       # 180,000 cycles in 100 us
+    assert d["mfma_share"] == pytest.approx(0.5)
+    assert d["lds_share"] == pytest.approx(0.2)
+    assert d["cu_share"] == pytest.approx(0.9)
+    assert d["body_share"] == pytest.approx((55000 - 100000) / (-0.5 * 100000))   # 0.9
+    assert d["dram_share"] == pytest.approx((100000 * 2048 / 8e12 + 50000 * 1024 / 4e12) / 1e-4)
+    short = dict(row, GRBM_GUI_ACTIVE=480000.0)                          # 4.8 GHz: the window, not the kernel
+    assert LC.derived3(short, hwj)["clock_hz"] == 2.4e9
+
+
+def test_registration_3_text_matches_the_code():
+    text = open(REG3.mapping).read()
+    assert "| 1 | DRAM share ≥ %.2f | `HBM` |" % LC.DRAM_SHARE_MIN_3 in text
+    assert "| 2 | CU share < %.2f | `WAVES` |" % LC.CU_SHARE_MIN_3 in text
+    assert "| 3 | body share < %.2f | `ENVELOPE` |" % LC.BODY_SHARE_MIN_3 in text
+    assert "| 4 | LDS share ≥ %.2f x MFMA share | `SMEM` |" % LC.LDS_OVER_MFMA_MIN_3 in text
+    assert "| 5 | MFMA share / min(1, body share) ≥ %.2f | `TENSOR_CORE` |" % LC.MFMA_OVER_BODY_MIN_3 in text
+    assert "| 6 | otherwise | `OCC` |" in text
+    n = len(LC.load_configs(REG3.configs)) - 1
+    assert "%d scored configs (%d of %d)" % (n, -(-75 * n // 100), n) in text
+    assert "[%.2f, %.2f]" % LC.CONTROL_CU_SHARE_3 in text
+    import json
+    assert json.load(open(REG3.hw_json)) == json.load(open(os.path.join(ROOT, "data", "sweep",
+                                                                         "mi355x-heldout5-hw.json")))
