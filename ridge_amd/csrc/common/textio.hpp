@@ -14,6 +14,7 @@
 #include <cstring>
 #include <fstream>
 #include <map>
+#include <set>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -46,8 +47,36 @@ inline Status readWholeFile(const std::string& path, std::string& text) {
 
 // ---------------------------------------------------------------- numbers --
 
-// The whole of `s` (surrounding blanks aside) as a finite real.
+// True when `s` (surrounding blanks aside) is a decimal number as JSON writes
+// one, with an optional leading '+': [+-]? digits [. digits]? ([eE] [+-]? digits)?.
+// strtod alone would also take hexadecimal ("0x1p3"), "inf" and "nan".
+inline bool isDecimalNumber(const std::string& s) {
+    size_t i = 0, n = s.size();
+    while (i < n && std::isspace(static_cast<unsigned char>(s[i]))) ++i;
+    while (n > i && std::isspace(static_cast<unsigned char>(s[n - 1]))) --n;
+    auto digits = [&]() {
+        const size_t from = i;
+        while (i < n && std::isdigit(static_cast<unsigned char>(s[i]))) ++i;
+        return i > from;
+    };
+    if (i < n && (s[i] == '-' || s[i] == '+')) ++i;
+    if (!digits()) return false;
+    if (i < n && s[i] == '.') {
+        ++i;
+        if (!digits()) return false;
+    }
+    if (i < n && (s[i] == 'e' || s[i] == 'E')) {
+        ++i;
+        if (i < n && (s[i] == '-' || s[i] == '+')) ++i;
+        if (!digits()) return false;
+    }
+    return i == n;
+}
+
+// The whole of `s` (surrounding blanks aside) as a finite real written in
+// decimal notation (isDecimalNumber).
 inline bool toReal(const std::string& s, double& v) {
+    if (!isDecimalNumber(s)) return false;
     const char* b = s.c_str();
     char* e = nullptr;
     errno = 0;
@@ -73,9 +102,12 @@ inline bool toInteger(const std::string& s, long long& v) {
 // Accepted: one object whose values are strings, numbers, true, false or null,
 // e.g. {"numSMs": 256, "name": "MI355X"}. Keys are unique. Nested objects and
 // arrays are refused (the format is flat by definition). String values are
-// stored unescaped; every other value is stored as written.
+// stored unescaped; every other value is stored as written. `quoted` names the
+// keys whose value was a string, so that a numeric field can refuse "256".
 
-using FlatObject = std::map<std::string, std::string>;
+struct FlatObject : std::map<std::string, std::string> {
+    std::set<std::string> quoted;
+};
 
 namespace detail {
 
@@ -193,6 +225,7 @@ inline Status parseFlatObject(const std::string& text, const std::string& source
                 if (t.kind != Token::Text && t.kind != Token::Scalar)
                     return fail(t, "key \"" + key + "\" has no value");
                 kv[key] = t.value;
+                if (t.kind == Token::Text) kv.quoted.insert(key);
                 want = Want::CommaOrClose;
                 break;
             case Want::CommaOrClose:
@@ -206,7 +239,7 @@ inline Status parseFlatObject(const std::string& text, const std::string& source
                 break;
             case Want::Nothing:
                 if (t.kind != Token::End) return fail(t, "text after the end of the object");
-                out.swap(kv);
+                out = std::move(kv);
                 return Status();
         }
     }

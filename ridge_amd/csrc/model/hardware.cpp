@@ -134,6 +134,8 @@ ridgeio::Status applySchema(const ridgeio::FlatObject& kv, const std::vector<Key
             if (rule.required) return ridgeio::Status::failure("", "required constant " + name + " is absent");
             continue;
         }
+        if (kv.quoted.count(rule.key))
+            return ridgeio::Status::failure("", name + " must be a number, found the string \"" + it->second + "\"");
         double value = 0.0;
         if (rule.integer) {
             long long n = 0;

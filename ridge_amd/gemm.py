@@ -191,8 +191,12 @@ def bound_launch(i, A, B, C, M, N, K, stream=None):
     timing loops whose launches are shorter than Python's argument handling."""
     f = lib().ridge_gemm_launch
     args = (i, _ptr(A), _ptr(B), _ptr(C), M, N, K, _stream_handle(stream))
+    # The closure holds the operands (and the stream object), so the raw
+    # pointers in `args` stay valid for as long as the callable exists.
+    keep = (A, B, C, stream)
 
     def call():
+        assert keep is not None
         rc = f(*args)
         if rc != HIP_SUCCESS:
             raise RidgeGemmError("ridge_gemm_launch(variant %d, %dx%dx%d) returned hipError %d" % (i, M, N, K, rc))
@@ -266,6 +270,8 @@ class BlasLt:
             raise RidgeGemmError("ridge_blaslt_prepare(%dx%dx%d) returned %d" % (M, N, K, rc))
 
     def gemm(self, A, B, C, M, N, K, c_is_f32=False, stream=None):
+        if not self._h:
+            raise RidgeGemmError("the hipBLASLt handle is closed")
         rc = lib().ridge_blaslt_gemm(self._h, _ptr(A), _ptr(B), _ptr(C), M, N, K, int(c_is_f32),
                                      _stream_handle(stream))
         if rc != 0:
@@ -273,10 +279,18 @@ class BlasLt:
 
     def bound_gemm(self, A, B, C, M, N, K, c_is_f32=False, stream=None):
         """gemm() as a zero-argument callable with its arguments converted once."""
+        if not self._h:
+            raise RidgeGemmError("the hipBLASLt handle is closed")
         f = lib().ridge_blaslt_gemm
         args = (self._h, _ptr(A), _ptr(B), _ptr(C), M, N, K, int(c_is_f32), _stream_handle(stream))
+        # The closure holds the operands and this object; a call after close()
+        # is refused instead of reaching a destroyed handle.
+        keep = (A, B, C, stream)
 
         def call():
+            assert keep is not None
+            if not self._h:
+                raise RidgeGemmError("the hipBLASLt handle is closed")
             rc = f(*args)
             if rc != 0:
                 raise RidgeGemmError("ridge_blaslt_gemm(%dx%dx%d) returned %d" % (M, N, K, rc))

@@ -158,3 +158,31 @@ def test_binding_struct_layouts_match_the_libraries():
                                                              "mallStretch", "kernelSeconds", "dramReadBytes",
                                                              "dramWriteBytes", "dramShare", "bodyFactor",
                                                              "bodyShare", "cuShare", "mfmaShare", "ldsShare"]
+
+
+def test_bound_callables_hold_their_operands_and_refuse_a_closed_handle():
+    """A bound launch keeps the objects whose raw pointers it converted alive for
+    as long as it exists (no GPU call is made here), and a bound or direct
+    hipBLASLt call on a closed handle is refused before reaching the library."""
+    import gc
+    import weakref
+
+    class Operand:
+        def data_ptr(self):
+            return 0
+
+    a = Operand()
+    ref = weakref.ref(a)
+    call = G.bound_launch(0, a, Operand(), Operand(), 256, 256, 64, stream=0)
+    del a
+    gc.collect()
+    assert ref() is not None
+    del call
+    gc.collect()
+    assert ref() is None
+    closed = G.BlasLt.__new__(G.BlasLt)
+    closed._h = None
+    with pytest.raises(G.RidgeGemmError, match="closed"):
+        closed.bound_gemm(Operand(), Operand(), Operand(), 256, 256, 64, stream=0)
+    with pytest.raises(G.RidgeGemmError, match="closed"):
+        closed.gemm(Operand(), Operand(), Operand(), 256, 256, 64, stream=0)

@@ -311,3 +311,24 @@ def test_registration_3_text_matches_the_code():
     import json
     assert json.load(open(REG3.hw_json)) == json.load(open(os.path.join(ROOT, "data", "sweep",
                                                                          "mi355x-heldout5-hw.json")))
+
+
+def test_registration_3_counters_score_as_reported():
+    """Registration 3's committed counters through its registered table: 19 of 26
+    agree, FAIL (20 needed); 17 of the 23 held-out configs; the control in band."""
+    import json
+    with open(REG3.hw_json) as f:
+        hwj = json.load(f)
+    rows = LC._read_rows(REG3.counters)
+    results, agree, need, control_ok = LC.score(rows, hwj, 3)
+    assert control_ok and (agree, need) == (19, 20)
+    split = {}
+    for r, d, lab in results:
+        if r["predicted_label"] != "CONTROL":
+            s = split.setdefault(r["predicted_label"], [0, 0])
+            s[0] += lab == r["predicted_label"]
+            s[1] += 1
+    assert split == {"HBM": [4, 5], "WAVES": [4, 4], "ENVELOPE": [3, 4], "SMEM": [4, 5], "TENSOR_CORE": [0, 4],
+                     "OCC": [4, 4]}
+    fresh = [(r, lab) for r, d, lab in results if r["why"] == "per-label rule"]
+    assert len(fresh) == 23 and sum(lab == r["predicted_label"] for r, lab in fresh) == 17

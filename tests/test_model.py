@@ -320,13 +320,20 @@ def test_hardware_json_loader_is_all_or_nothing(tmp_path):
     # The reader's own error model: every failure names the file and what is wrong.
     for text, why in [
         (good.read_text().replace('"numSMs": 256', '"numSMs": 256.5'), '"numSMs" must be an integer'),
-        (good.read_text().replace('"numSMs": 256', '"numSMs": "many"'), '"numSMs" must be an integer'),
+        (good.read_text().replace('"numSMs": 256', '"numSMs": "many"'), '"numSMs" must be a number'),
         (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 2.1e9, "clockHz": 1e9'), "appears twice"),
         (good.read_text().replace('"name": "x"', '"name": {"a": 1}'), "nested objects"),
         (good.read_text().replace('"name": "x"', '"name": [1]'), "arrays"),
         (good.read_text() + " {}", "after the end"),
         (good.read_text().rstrip().rstrip("}"), "not closed"),
         (good.read_text().replace('"clockHz": 2.1e9', '"clockHz" 2.1e9'), "':' belongs after"),
+        # A number in quotes, and forms strtod takes but JSON does not write.
+        (good.read_text().replace('"numSMs": 256', '"numSMs": "256"'), '"numSMs" must be a number, found the string'),
+        (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": "2.1e9"'), '"clockHz" must be a number'),
+        (good.read_text().replace('"numSMs": 256', '"numSMs": 0x100'), "neither a number"),
+        (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 0x1p31'), "neither a number"),
+        (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": inf'), "neither a number"),
+        (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 2.e9'), "neither a number"),
     ]:
         broken = tmp_path / "broken.json"
         broken.write_text(text)
