@@ -124,11 +124,15 @@ struct HardwareModel {
                                      //    back-to-back sequence (the measurement protocol of the sweeps)
     double launchOverheadSeconds = 0.0;  // [CAL] per launch on top of its work, back to back (cal-latency)
     double launchIsolatedSeconds = 0.0;  // [CAL] the same for one launch from an idle stream (cal-latency)
+    double nominalClockHz = 0.0;     // engine clock ceiling (cal-mma reports the device's), read by labelModel 1
     int labelModel = 0;              // 0: the label names the derating furthest from 1 (reference :129-143)
                                      // 1: the label is the counter decision table applied to the model's
                                      //    own prediction of what the counters read on one launch from an
                                      //    idle stream: DRAM share, body share from a second K, CU share,
                                      //    LDS and MFMA busy shares (Prediction's observable fields)
+                                     // 2: the same, the busy shares counted at the physical clock: from
+                                     //    nominalClockHz (matrix pipes idle) to clockHz x loadedClockRatio
+                                     //    (always busy), linear in the row's matrix load
 
     // Datasheet placeholders of the reference (hardware.cpp:19-34).
     static HardwareModel a100();

@@ -74,6 +74,8 @@ struct Prediction {
     double cuShare = 0.0;              // CU-time share the grid keeps occupied
     double mfmaShare = 0.0;            // matrix-pipe busy share of the SIMD cycles
     double ldsShare = 0.0;             // LDS busy share of the CU cycles (fragment reads)
+    double matrixLoad = 0.0;           // share of the time the matrix pipes are busy (the power term's u)
+    double observedClockHz = 0.0;      // the clock the counters count at under that load
 };
 
 }  // namespace ridge

@@ -50,7 +50,7 @@ typedef struct ridge_model_prediction {
     double mallStretch;      /* K-step stretch from the calibrated curve (mallStreamModel 1) */
     /* What the counters read on one launch from an idle stream (labelModel 1; 0 otherwise). */
     double kernelSeconds, dramReadBytes, dramWriteBytes, dramShare, bodyFactor, bodyShare, cuShare, mfmaShare,
-        ldsShare;
+        ldsShare, matrixLoad, observedClockHz;
 } ridge_model_prediction_t;
 
 /* Default config (the reference's GemmConfig defaults, config.h:18-39). */

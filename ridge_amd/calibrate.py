@@ -240,6 +240,9 @@ def hardware_json(res, spec, arch):
                         ("labelModel", ["launchIsolatedSeconds", "hbmWriteBytesPerSec"])):
         if all(k in res for k in needs):
             out[term] = 1
+    if out.get("labelModel") == 1 and "nominalClockHz" in res:
+        # The busy shares at the physical clock of the row's matrix load.
+        out["labelModel"] = 2
     for key in SKELETON_KEYS:
         if key in res:
             out[key] = res[key]

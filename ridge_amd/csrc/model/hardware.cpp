@@ -123,6 +123,7 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         I("fillShareModel", h.fillShareModel), I("mallReuseModel", h.mallReuseModel), R("mallBytes", h.mallBytes),
         I("launchModel", h.launchModel), R("launchOverheadSeconds", h.launchOverheadSeconds),
         R("launchIsolatedSeconds", h.launchIsolatedSeconds), I("labelModel", h.labelModel),
+        R("nominalClockHz", h.nominalClockHz),
     };
 }
 
@@ -194,6 +195,10 @@ std::string inconsistency(const HardwareModel& h) {
     if (h.labelModel == 1 && !(h.launchIsolatedSeconds >= 0.0 && h.hbmWriteModel == 1 && h.simdsPerSM > 0))
         return "labelModel 1 reads launchIsolatedSeconds (not negative) and needs hbmWriteModel 1 and per-SIMD "
                "register files (simdsPerSM > 0)";
+    if (h.labelModel == 2 && !(h.launchIsolatedSeconds >= 0.0 && h.hbmWriteModel == 1 && h.simdsPerSM > 0 &&
+                               h.powerModel == 1 && h.nominalClockHz >= h.clockHz))
+        return "labelModel 2 reads launchIsolatedSeconds (not negative) and nominalClockHz (at least clockHz), and "
+               "needs hbmWriteModel 1, powerModel 1 and per-SIMD register files (simdsPerSM > 0)";
     return "";
 }
 

@@ -78,7 +78,9 @@
 //                           (DRAM share, body share from a second K, CU share,
 //                           MFMA and LDS busy shares) and labels that prediction
 //                           with the counters' decision table (reference: the
-//                           derating furthest from 1, :129-143)
+//                           derating furthest from 1, :129-143); labelModel 2
+//                           counts the busy shares at the physical clock of the
+//                           row's matrix load instead of the loaded clock
 //
 // With the defaults (a100() or a reference JSON) every term reduces to the
 // reference's expression in the same double-precision operation order, so the
@@ -438,6 +440,7 @@ Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
         // MFMA stream's; a row that keeps the pipes busy a share u of the time
         // pays that share of the drop.
         const double u = std::min(1.0, computeTFLOPS / peakTensorTFLOPS);
+        p.matrixLoad = u;
         p.powerClockFactor = 1.0 - (1.0 - hw.loadedClockRatio) * u;
         computeTFLOPS *= p.powerClockFactor;
     }
@@ -629,10 +632,21 @@ void observe(const GemmConfig& cfg, const HardwareModel& hw, Prediction& p) {
         p.cuShare = ((rounds - 1.0) + std::min(1.0, tail / cus)) / rounds;
     }
 
-    // Busy shares at the model's loaded clock: every MFMA costs its issue
-    // cycles on one SIMD, every K-step its fragment reads on the CU's LDS.
+    // Busy shares: every MFMA costs its issue cycles on one SIMD, every K-step
+    // its fragment reads on the CU's LDS, over the cycles of the duration.
+    // labelModel 1 counts those at the model's loaded clock. labelModel 2 counts
+    // them at the clock the counters see: with the matrix pipes idle the engine
+    // runs at nominalClockHz, with them always busy (and the GEMM's data
+    // movement) at the calibrated skeleton's clockHz x loadedClockRatio, and a
+    // row whose pipes are busy a share u of the time between the two. (The
+    // throughput terms keep the loaded clock their cycle counts were calibrated
+    // at; the counters count physical cycles.)
     const MmaShape mma = mmaShapeFor(cfg.dtype, hw);
-    const double clock = hw.clockHz * p.powerClockFactor;
+    const double clock =
+        hw.labelModel == 2
+            ? hw.nominalClockHz + (hw.clockHz * hw.loadedClockRatio - hw.nominalClockHz) * p.matrixLoad
+            : hw.clockHz * p.powerClockFactor;
+    p.observedClockHz = clock;
     const double simds = cus * hw.simdsPerSM;
     const double mfmaCyclesPerSimd = flops / double(mma.flops) * hw.mmaCyclesPerInst * hw.simdsPerSM / simds;
     p.mfmaShare = mfmaCyclesPerSimd / (p.kernelSeconds * clock);
@@ -656,7 +670,7 @@ void observe(const GemmConfig& cfg, const HardwareModel& hw, Prediction& p) {
 
 Prediction predict(const GemmConfig& cfg, const HardwareModel& hw) {
     Prediction p = predictCore(cfg, hw);
-    if (hw.labelModel == 1 && p.bottleneck != Bottleneck::DoesNotFit) observe(cfg, hw, p);
+    if ((hw.labelModel == 1 || hw.labelModel == 2) && p.bottleneck != Bottleneck::DoesNotFit) observe(cfg, hw, p);
     return p;
 }
 

@@ -142,6 +142,8 @@ int ridge_model_predict(const void* hwp, const ridge_model_config_t* cfg, ridge_
     out->cuShare = p.cuShare;
     out->mfmaShare = p.mfmaShare;
     out->ldsShare = p.ldsShare;
+    out->matrixLoad = p.matrixLoad;
+    out->observedClockHz = p.observedClockHz;
     return 0;
 }
 

@@ -93,8 +93,16 @@ def body_factors(c):
 
 REGISTRATIONS = {1: Registration(1, "rocprof-label", 0), 2: Registration(2, "rocprof-label2", 16),
                  3: Registration(3, "rocprof-label3", factors=body_factors),
+                 4: Registration(4, "rocprof-label4", factors=body_factors),
                  "design": Registration("design", "rocprof-label-design", factors=design_factors)}
-CURRENT = 3
+CURRENT = 4
+# Registrations 3 and 4 share the decision table; each draws its fresh configs
+# from the cross product of a held-out sweep registered with it.
+REGISTRATIONS[3].heldout_shapes = os.path.join(SWEEP_DIR, "mi355x-heldout5-registered.csv")
+REGISTRATIONS[4].heldout_shapes = os.path.join(SWEEP_DIR, "mi355x-heldout6-registered.csv")
+for _r in (REGISTRATIONS[3], REGISTRATIONS[4]):
+    _r.table = os.path.join(SWEEP_DIR, _r.stem + "-table.csv")
+TABLE_RULE_REGISTRATIONS = (3, 4)
 # Registration 1's files under their original names (kept for its tests).
 HW_JSON = REGISTRATIONS[1].hw_json
 SOURCES = REGISTRATIONS[1].sources
@@ -200,7 +208,7 @@ def select_configs3(reg):
     groupM) and the first PER_LABEL of distinct shapes are taken. The control and
     the BASELINE configs' best rows (REQUIRED_3) come first."""
     hw = RM.Hardware(reg.hw_json)
-    table = [{k: int(v) for k, v in r.items()} for r in _read_rows(TABLE3)]
+    table = [{k: int(v) for k, v in r.items()} for r in _read_rows(reg.table)]
     by_key = {tuple(t[k] for k in KEY_FIELDS): t for t in table}
 
     def config(M, N, K, t, tag):
@@ -221,7 +229,7 @@ def select_configs3(reg):
         r, p = config(key[0], key[1], key[2], by_key[key[3:]], tag)
         out.append(row("CONTROL" if why.startswith("control") else p["bottleneck"], r, p, why))
     groups = {}
-    for M, N, K, tag in T.read_shapes(HELDOUT5_SHAPES):
+    for M, N, K, tag in T.read_shapes(reg.heldout_shapes):
         for t in table:
             r, p = config(M, N, K, t, tag)
             groups.setdefault(p["bottleneck"], []).append((r, p))
@@ -339,7 +347,7 @@ def cmd_select(args):
     if reg.number == "design":
         rows = design_configs()
         note = "label-design set (in-sample, never scored); see ridge_amd/labelcheck.py design_configs"
-    elif reg.number == 3:
+    elif reg.number in TABLE_RULE_REGISTRATIONS:
         rows = select_configs3(reg)
         note = "registered before any rocprofv3 run; see %s" % os.path.relpath(reg.mapping, ROOT)
     else:
@@ -589,7 +597,7 @@ def derived3(row, hwj):
     d["lds_share"] = float(row["SQ_LDS_IDX_ACTIVE"]) / (cus * dur * clock)
     d["cu_share"] = float(row["SQ_BUSY_CU_CYCLES"]) / (cus * dur * clock)
     f = body_factors({"K": int(row["K"]), "BK": int(row["BK"])})[1]
-    t2 = float(row[REGISTRATIONS[3].duration_column(f)]) * 1e-9
+    t2 = float(row[Registration.duration_column(REGISTRATIONS[3], f)]) * 1e-9
     d["body_factor"] = f
     d["body_share"] = (t2 - dur) / ((f - 1.0) * dur)
     return d
@@ -620,7 +628,7 @@ def score(rows, hwj, registration=1):
     control_ok = True
     reg = REGISTRATIONS[registration]
     for r in rows:
-        if registration == 3:
+        if registration in TABLE_RULE_REGISTRATIONS:
             d = derived3(r, hwj)
             results.append((r, d, counter_label3(d)))
             if r["predicted_label"] == "CONTROL":
@@ -677,7 +685,7 @@ def cmd_score(args):
         hwj = json.load(f)
     rows = _read_rows(args.counters_csv or reg.counters)
     results, agree, need, control_ok = score(rows, hwj, reg.number)
-    if reg.number == 3:
+    if reg.number in TABLE_RULE_REGISTRATIONS:
         return _print_score3(results, agree, need, control_ok)
     print("%-9s %-28s %-22s %6s %6s %6s %6s %6s %6s %6s  %-9s" % (
         "model", "shape", "variant", "HBM%", "SIMD%", "occ%", "theo%", "LDS%", "MFMA%", "steady", "counters"))

@@ -35,7 +35,8 @@ _PRED_FIELDS = [("predictedTFLOPS", ctypes.c_double), ("bottleneck", ctypes.c_in
                                     "compulsoryIntensity", "tailClockFactor", "l2HitBytes", "powerClockFactor",
                                     "fillRounds", "refillMissShare", "mallLoad", "mallStretch",
                                     "kernelSeconds", "dramReadBytes", "dramWriteBytes", "dramShare", "bodyFactor",
-                                    "bodyShare", "cuShare", "mfmaShare", "ldsShare")]
+                                    "bodyShare", "cuShare", "mfmaShare", "ldsShare", "matrixLoad",
+                                    "observedClockHz")]
 
 
 class _Prediction(ctypes.Structure):

@@ -153,11 +153,12 @@ def test_binding_struct_layouts_match_the_libraries():
     assert L.ridge_model_prediction_size() == ctypes.sizeof(RM._Prediction)
     # The prediction ends with the gfx950 fields, after the reference's, and the
     # counter observables last.
-    assert [f for f, _ in RM._Prediction._fields_][-16:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor",
+    assert [f for f, _ in RM._Prediction._fields_][-18:] == ["tailClockFactor", "l2HitBytes", "powerClockFactor",
                                                              "fillRounds", "refillMissShare", "mallLoad",
                                                              "mallStretch", "kernelSeconds", "dramReadBytes",
                                                              "dramWriteBytes", "dramShare", "bodyFactor",
-                                                             "bodyShare", "cuShare", "mfmaShare", "ldsShare"]
+                                                             "bodyShare", "cuShare", "mfmaShare", "ldsShare",
+                                                             "matrixLoad", "observedClockHz"]
 
 
 def test_bound_callables_hold_their_operands_and_refuse_a_closed_handle():

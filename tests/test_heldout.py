@@ -284,3 +284,28 @@ def test_fifth_heldout_figures_as_reported():
     assert base[1]["random"][0] == pytest.approx(22.91, abs=0.01)
     before = V.join(MEASURED5, FROZEN4)
     assert sum(j.abs_pct for j in before) / len(before) == pytest.approx(11.06, abs=0.01)
+
+
+# The sixth held-out sweep (data/sweep/mi355x-heldout6.md).
+REGISTERED6 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout6-registered.csv")
+FROZEN6 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout6-hw.json")
+TABLE6 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout6-table.csv")
+
+
+def test_sixth_heldout_registration():
+    """14 shapes no earlier set or BASELINE config holds, the fifth set's table and
+    constants with labelModel 2, which leaves every prediction unchanged."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED6)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    assert len(held) == 14 and not held & earlier
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE6) == keys(TABLE5)
+    five, six = json.load(open(FROZEN5)), json.load(open(FROZEN6))
+    assert {k: v for k, v in six.items() if k != "labelModel"} == {k: v for k, v in five.items() if k != "labelModel"}
+    assert six["labelModel"] == 2
+    a, b = V.join(MEASURED5, FROZEN5), V.join(MEASURED5, FROZEN6)
+    assert [j.predicted for j in a] == [j.predicted for j in b]

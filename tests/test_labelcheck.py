@@ -332,3 +332,31 @@ def test_registration_3_counters_score_as_reported():
                      "OCC": [4, 4]}
     fresh = [(r, lab) for r, d, lab in results if r["why"] == "per-label rule"]
     assert len(fresh) == 23 and sum(lab == r["predicted_label"] for r, lab in fresh) == 17
+
+
+REG4 = LC.REGISTRATIONS[4]
+
+
+def test_registration_4_configs_are_its_selection(tmp_path):
+    """Registration 4 re-derives from its frozen files with registration 3's rule
+    (the sixth held-out sweep, the same frozen table); its text is registration
+    3's table, quantities and criterion."""
+    out = tmp_path / "c4.csv"
+    LC.main(["--registration", "4", "select", "--out", str(out)])
+    assert LC._read_rows(str(out)) == LC._read_rows(REG4.configs)
+    rows = LC.load_configs(REG4.configs)
+    assert rows[0]["predicted_label"] == "CONTROL" and len(rows) - 1 == 26
+    heldout = {(m, n, k) for m, n, k, _ in LC.T.read_shapes(REG4.heldout_shapes)}
+    assert all((r["M"], r["N"], r["K"]) in heldout for r in rows[4:])
+    assert all(r["model_label"] == r["predicted_label"] for r in rows[1:])
+    assert LC._read_rows(REG4.table) == LC._read_rows(REG3.table)
+    text3, text4 = open(REG3.mapping).read(), open(REG4.mapping).read()
+    for start, end in (("## 3. Decision procedure", "**Control.**"), ("## 5. Pass criterion", "## 6.")):
+        sec = lambda t: t[t.index(start):t.index(end)]  # noqa: E731
+        assert sec(text4).replace("labelModel 2", "labelModel 1") == sec(text3)
+    import json
+    hw4 = json.load(open(REG4.hw_json))
+    assert hw4["labelModel"] == 2 and hw4 == json.load(open(os.path.join(ROOT, "data", "sweep",
+                                                                         "mi355x-heldout6-hw.json")))
+    hw3 = json.load(open(REG3.hw_json))
+    assert {k: v for k, v in hw4.items() if k != "labelModel"} == {k: v for k, v in hw3.items() if k != "labelModel"}

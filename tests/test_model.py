@@ -847,3 +847,35 @@ def test_label_model_is_the_registered_counter_table(mi355x_calibrated):
             assert LC.counter_label3(obs) == p["bottleneck"], r
             seen.add(p["bottleneck"])
     assert {"HBM", "WAVES", "ENVELOPE", "SMEM", "TENSOR_CORE"} <= seen
+
+
+def test_label_model_2_counts_busy_shares_at_the_physical_clock(tmp_path):
+    """labelModel 2 with powerModel 1 (loadedClockRatio 0.75), clockHz 2.4 GHz and
+    nominalClockHz 3.0 GHz: a row whose matrix pipes the power term sees busy a
+    share u runs, as the counters count, at 3.0 + (2.4 x 0.75 - 3.0) u GHz, and its
+    MFMA and LDS shares are labelModel 1's scaled by (2.4 GHz x powerClockFactor) /
+    that clock; the duration, DRAM, body and CU shares are unchanged."""
+    base = _LABEL_JSON + ', "powerModel": 1, "loadedClockRatio": 0.75, "nominalClockHz": 3.0e9'
+    one, two = tmp_path / "one.json", tmp_path / "two.json"
+    one.write_text(_CDNA4_JSON % base)
+    two.write_text(_CDNA4_JSON % base.replace('"labelModel": 1', '"labelModel": 2'))
+    h1, h2 = RM.Hardware(str(one)), RM.Hardware(str(two))
+    for cfg in (dict(M=4096, N=4096, K=4096, BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=3, regsPerThread=200,
+                     groupM=4, schedule=1),
+                dict(M=4096, N=2048, K=8192, BM=128, BN=256, BK=32, warpM=64, warpN=128, stages=4, regsPerThread=180,
+                     groupM=8)):
+        a, b = RM.predict(h1, **cfg), RM.predict(h2, **cfg)
+        u = a["matrixLoad"]
+        assert a["powerClockFactor"] == pytest.approx(1.0 - 0.25 * u)
+        clock = 3.0e9 + (2.4e9 * 0.75 - 3.0e9) * u
+        assert b["observedClockHz"] == pytest.approx(clock)
+        assert a["observedClockHz"] == pytest.approx(2.4e9 * a["powerClockFactor"])
+        k = 2.4e9 * a["powerClockFactor"] / clock
+        assert b["mfmaShare"] == pytest.approx(a["mfmaShare"] * k)
+        assert b["ldsShare"] == pytest.approx(a["ldsShare"] * k)
+        for key in ("predictedTFLOPS", "kernelSeconds", "dramShare", "bodyShare", "cuShare"):
+            assert b[key] == a[key], key
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % base.replace('"labelModel": 1', '"labelModel": 2').replace("3.0e9", "2.0e9"))
+    with pytest.raises(ValueError, match="labelModel 2"):
+        RM.Hardware(str(bad))
