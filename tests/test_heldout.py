@@ -309,3 +309,27 @@ def test_sixth_heldout_registration():
     assert six["labelModel"] == 2
     a, b = V.join(MEASURED5, FROZEN5), V.join(MEASURED5, FROZEN6)
     assert [j.predicted for j in a] == [j.predicted for j in b]
+
+
+MEASURED6 = os.path.join(ROOT, "data", "measured", "mi355x-heldout6.csv")
+
+
+def test_sixth_heldout_figures_as_reported():
+    """Measured once as registered (canary range 3.5%): MAPE 8.78%, k = 10 finds
+    every shape's best (and k = 5 already), regret at k = 1 2.04% mean and 15.43%
+    worst (1024 x 1024 x 4096, a 16-tile-wide grid of 64x64 rows)."""
+    frozen = T.read(TABLE6, require=V.KEY_COLUMNS)
+    keys = [tuple(frozen.number(i, c, int) for c in V.KEY_COLUMNS) for i in range(len(frozen))]
+    table = T.read(MEASURED6)
+    absent, unexpected = V.registered_gate(table.records, T.read_shapes(REGISTERED6), keys)
+    assert not absent and not unexpected and float(table.meta["canary_drift_fraction"]) <= 0.05
+    rows = V.join(MEASURED6, FROZEN6)
+    assert sum(j.abs_pct for j in rows) / len(rows) == pytest.approx(8.78, abs=0.01)
+    result, total, shapes, _ = AT.evaluate(MEASURED6, FROZEN6, ks=(1, 5, 10))
+    by_k = {r["k"]: r for r in result}
+    assert (total, shapes) == (336, 14)
+    assert by_k[1]["mean_regret"] == pytest.approx(2.04, abs=0.01) and by_k[1]["hits"] == 8
+    assert by_k[1]["max_regret"] == pytest.approx(15.43, abs=0.01)
+    assert by_k[5]["mean_regret"] == 0.0 and by_k[10]["mean_regret"] == 0.0 and by_k[10]["hits"] == 14
+    base = AT.baselines(MEASURED6, FROZEN6, ks=(1, 10))
+    assert base[1]["random"][0] == pytest.approx(26.21, abs=0.01)

@@ -360,3 +360,24 @@ def test_registration_4_configs_are_its_selection(tmp_path):
                                                                          "mi355x-heldout6-hw.json")))
     hw3 = json.load(open(REG3.hw_json))
     assert {k: v for k, v in hw4.items() if k != "labelModel"} == {k: v for k, v in hw3.items() if k != "labelModel"}
+
+
+def test_registration_4_counters_score_as_reported():
+    """Registration 4's committed counters through the registered table: 22 of 26
+    agree, PASS (20 needed); 20 of the 23 held-out configs; the control in band."""
+    import json
+    with open(REG4.hw_json) as f:
+        hwj = json.load(f)
+    rows = LC._read_rows(REG4.counters)
+    results, agree, need, control_ok = LC.score(rows, hwj, 4)
+    assert control_ok and (agree, need) == (22, 20)
+    split = {}
+    for r, d, lab in results:
+        if r["predicted_label"] != "CONTROL":
+            s = split.setdefault(r["predicted_label"], [0, 0])
+            s[0] += lab == r["predicted_label"]
+            s[1] += 1
+    assert split == {"HBM": [4, 4], "WAVES": [4, 4], "ENVELOPE": [2, 5], "SMEM": [4, 5], "TENSOR_CORE": [4, 4],
+                     "OCC": [4, 4]}
+    fresh = [(r, lab) for r, d, lab in results if r["why"] == "per-label rule"]
+    assert len(fresh) == 23 and sum(lab == r["predicted_label"] for r, lab in fresh) == 20
