@@ -381,3 +381,18 @@ def test_registration_4_counters_score_as_reported():
                      "OCC": [4, 4]}
     fresh = [(r, lab) for r, d, lab in results if r["why"] == "per-label rule"]
     assert len(fresh) == 23 and sum(lab == r["predicted_label"] for r, lab in fresh) == 20
+
+
+def test_in_sample_relabelling_figures():
+    """The in-sample figures the registrations quote, from committed counters: the
+    design set (61 configs, never scored) agrees on 55 under the current model and
+    under registration 3's frozen calibration; registration 3's counters, relabelled
+    by the current model, agree on 21 of 26 (their registered score stays 19)."""
+    design = LC._read_rows(LC.REGISTRATIONS["design"].counters)
+    assert len(design) == 61 and all(r["predicted_label"] == "DESIGN" for r in design)
+    current = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+    for hw in (current, REG3.hw_json):
+        results, agree, need, _ = LC.relabel_in_sample(design, hw)
+        assert (agree, need) == (55, None)
+    results, agree, _, _ = LC.relabel_in_sample(LC._read_rows(REG3.counters), current)
+    assert agree == 21 and sum(r["predicted_label"] != "CONTROL" for r, d, lab in results) == 26
