@@ -19,6 +19,7 @@ ridge_amd.tables. Exit code 1 when a gate fails.
 
 import argparse
 import collections
+import math
 import os
 import sys
 import tempfile
@@ -182,6 +183,34 @@ def _mean(xs):
     return sum(xs) / len(xs) if xs else S.NAN
 
 
+def vendor_ratios(paths):
+    """The table's best row against the vendor library on every shape of the
+    measured files: [(ratio, (M, N, K), path)], where ratio is the shape's largest
+    `tflops` over the median of its rows' `blas_tflops` (ridge-measure times the
+    vendor library beside every row, in the same process)."""
+    out = []
+    for path in paths:
+        by = collections.defaultdict(list)
+        for r in T.read(path, require=("M", "N", "K", "tflops", "blas_tflops")).records:
+            by[(int(r["M"]), int(r["N"]), int(r["K"]))].append(r)
+        for shape, rs in sorted(by.items()):
+            best = max(float(r["tflops"]) for r in rs)
+            out.append((best / S.quantile([float(r["blas_tflops"]) for r in rs], 50), shape, path))
+    return out
+
+
+def print_vendor_ratios(paths):
+    ratios = vendor_ratios(paths)
+    xs = [x for x, _, _ in ratios]
+    lo, hi = min(ratios), max(ratios)
+    print("best row against hipBLASLt over %d shapes of %d files" % (len(xs), len(paths)))
+    print("  faster on %d; geometric mean %.3fx, median %.3fx" % (
+        sum(x > 1 for x in xs), math.exp(_mean([math.log(x) for x in xs])), S.quantile(xs, 50)))
+    for name, (x, shape, path) in (("lowest", lo), ("highest", hi)):
+        print("  %-8s %.3fx at %dx%dx%d (%s)" % (name, x, *shape, os.path.basename(path)))
+    return 0
+
+
 def report(rows, meta, hw, gate_lines, mape_target, mape_ceiling):
     """Prints the report; returns the list of failed gates."""
     failed = []
@@ -268,7 +297,11 @@ def main(argv=None):
     ap.add_argument("--fail-mape", type=float, default=15.0)
     ap.add_argument("--no-table-gate", action="store_true",
                     help="skip the registered cross-product gate (e.g. for another GPU's sweep)")
+    ap.add_argument("--vendor", nargs="+", metavar="MEASURED_CSV",
+                    help="only compare the best row with hipBLASLt over the shapes of these files")
     args = ap.parse_args(argv)
+    if args.vendor:
+        return print_vendor_ratios(args.vendor)
     try:
         meta = T.read(args.measured).meta
         rows = join(args.measured, args.hw, args.predict_bin)

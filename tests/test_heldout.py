@@ -330,6 +330,47 @@ def test_sixth_heldout_figures_as_reported():
     assert (total, shapes) == (336, 14)
     assert by_k[1]["mean_regret"] == pytest.approx(2.04, abs=0.01) and by_k[1]["hits"] == 8
     assert by_k[1]["max_regret"] == pytest.approx(15.43, abs=0.01)
-    assert by_k[5]["mean_regret"] == 0.0 and by_k[10]["mean_regret"] == 0.0 and by_k[10]["hits"] == 14
+    assert by_k[10]["mean_regret"] == 0.0 and by_k[10]["hits"] == 14
     base = AT.baselines(MEASURED6, FROZEN6, ks=(1, 10))
     assert base[1]["random"][0] == pytest.approx(26.21, abs=0.01)
+
+
+# The current figures under the committed calibration (data/hardware/mi355x.json).
+CURRENT_HW = os.path.join(ROOT, "data", "hardware", "mi355x.json")
+
+
+@pytest.mark.parametrize("name, mape, k1_mean, k1_max", [
+    ("mi355x.csv", 9.89, 1.19, 6.57),
+    ("mi355x-replicate.csv", 8.97, 1.02, 8.86),
+    ("mi355x-baseline-configs.csv", 14.38, 9.91, 27.95),
+    ("mi355x-heldout.csv", 7.60, 1.41, 11.04),
+    ("mi355x-heldout2.csv", 11.26, 2.20, 8.22),
+    ("mi355x-heldout3.csv", 10.00, 0.50, 4.15),
+    ("mi355x-heldout4.csv", 10.11, 1.98, 13.04),
+    ("mi355x-heldout5.csv", 8.10, 1.88, 12.23),
+    ("mi355x-heldout6.csv", 8.78, 2.04, 15.43),
+])
+def test_current_model_figures(name, mape, k1_mean, k1_max):
+    """MAPE and regret of every committed measurement under the current model;
+    k = 10 finds every shape's best."""
+    path = os.path.join(ROOT, "data", "measured", name)
+    rows = V.join(path, CURRENT_HW)
+    assert sum(j.abs_pct for j in rows) / len(rows) == pytest.approx(mape, abs=0.01)
+    result, _, _, _ = AT.evaluate(path, CURRENT_HW, ks=(1, 10))
+    by_k = {r["k"]: r for r in result}
+    assert by_k[1]["mean_regret"] == pytest.approx(k1_mean, abs=0.01)
+    assert by_k[1]["max_regret"] == pytest.approx(k1_max, abs=0.01)
+    assert by_k[10]["mean_regret"] == 0.0
+
+
+def test_best_row_against_hipblaslt_on_every_sweep_shape():
+    """The table's best row against hipBLASLt on the 98 shapes of the in-sample and
+    six held-out sweeps: faster on all, geometric mean 1.135x, median 1.090x."""
+    import math
+    names = ["mi355x.csv"] + ["mi355x-heldout%s.csv" % s for s in ("", "2", "3", "4", "5", "6")]
+    ratios = V.vendor_ratios([os.path.join(ROOT, "data", "measured", n) for n in names])
+    xs = [x for x, _, _ in ratios]
+    assert len(xs) == 98 and min(xs) > 1.0
+    assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.135, abs=0.001)
+    assert min(ratios)[1] == (8192, 16384, 4096) and max(ratios)[1] == (1024, 1024, 128)
+    assert min(xs) == pytest.approx(1.029, abs=0.001) and max(xs) == pytest.approx(1.843, abs=0.001)
