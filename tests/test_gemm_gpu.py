@@ -356,6 +356,40 @@ def test_largest_k_the_offset_guard_admits_is_exact():
     torch.cuda.empty_cache()
 
 
+def test_largest_n_the_offset_guard_admits_is_exact_on_bk128_persistent_rows():
+    """The BK = 128 persistent rows at the largest N the guard admits (BK * N just
+    under 2^31, so a B tile's last row starts just under 2^32 bytes from its first),
+    with two row panels and K = 2 BK, so the loaders' staggered K start reads the
+    second K tile first on one panel. A[i, k] = 1 where k = i (mod BK): row i sums
+    B rows i % BK and i % BK + BK. B[k, j] = 1 where k + j = 0 (mod 3), so every
+    output is 0, 1 or 2 and exact, and a wrapped or misplaced offset (a shift of a
+    whole K slice, or of 2^31 halves) reads another class. Checked on the device,
+    every output; B is about 8.6 GB and C about 4.3 GB."""
+    rows = [v for v in G.variants() if v.schedule == 2 and v.BK == 128]
+    assert len(rows) == 2
+    for v in rows:
+        M, K = 2 * v.BM, 2 * v.BK
+        N = (0x7FFFFFFF // v.BK) // v.BN * v.BN
+        assert v.divides(M, N, K) and not v.divides(M, N + v.BN, K)
+        print("  %s at %dx%dx%d" % (v.label(), M, N, K), flush=True)
+        k = torch.arange(K, device=DEV)
+        A = (k[None, :] % v.BK == torch.arange(M, device=DEV)[:, None] % v.BK).to(torch.float16)
+        jm3 = torch.arange(N, device=DEV, dtype=torch.int32) % 3
+        B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+        for kk in range(K):
+            B[kk] = (jm3 == (-kk) % 3).to(torch.float16)
+        C = _run(v.index, A, B, M, N, K)
+        del B
+        bad = 0
+        for i in range(M):
+            r = i % v.BK
+            want = ((jm3 + r) % 3 == 0).to(torch.int32) + ((jm3 + r + v.BK) % 3 == 0).to(torch.int32)
+            bad += int((C[i].to(torch.int32) != want).sum().item())
+        assert bad == 0, "%s at N = %d: %d of %d outputs differ" % (v.label(), N, bad, M * N)
+        del A, C, jm3
+        torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 128),
                                    (16384, 128, 8192)])
 def test_baseline_configs_uniform_inputs(M, N, K):
