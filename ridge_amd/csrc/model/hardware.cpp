@@ -161,6 +161,26 @@ std::string inconsistency(const HardwareModel& h) {
     if (h.waveSize <= 0 || h.mmaM <= 0 || h.mmaN <= 0 || h.mmaK <= 0 || h.regGranule <= 0 || h.numXcds <= 0 ||
         h.cBytes <= 0 || h.simdsPerSM < 0 || (h.simdsPerSM > 0 && h.regsPerSimdLane <= 0))
         return "the target description (waveSize, mma shape, register files, XCDs, cBytes) is out of range";
+    // Every term switch takes only the values the model defines; any other value
+    // would silently mean "off".
+    const struct {
+        const char* name;
+        int value, max;
+    } switches[] = {
+        {"l2ReuseModel", h.l2ReuseModel, 2},     {"prologueModel", h.prologueModel, 1},
+        {"pingPongModel", h.pingPongModel, 1},   {"persistentModel", h.persistentModel, 1},
+        {"ldsReadModel", h.ldsReadModel, 1},     {"clockModel", h.clockModel, 1},
+        {"l2StreamModel", h.l2StreamModel, 1},   {"uniformOverlapModel", h.uniformOverlapModel, 1},
+        {"powerModel", h.powerModel, 1},         {"hbmWriteModel", h.hbmWriteModel, 1},
+        {"fillLatencyModel", h.fillLatencyModel, 1}, {"mallStreamModel", h.mallStreamModel, 1},
+        {"persistentStepModel", h.persistentStepModel, 1}, {"fillShareModel", h.fillShareModel, 1},
+        {"mallReuseModel", h.mallReuseModel, 1}, {"launchModel", h.launchModel, 1},
+        {"labelModel", h.labelModel, 2},
+    };
+    for (const auto& s : switches)
+        if (s.value < 0 || s.value > s.max)
+            return std::string(s.name) + " must be an integer from 0 to " + std::to_string(s.max) + ", found " +
+                   std::to_string(s.value);
     if (h.ldsReadModel == 1 && !(h.ldsAReadBytesPerCycle > 0.0 && h.ldsBTrReadBytesPerCycle > 0.0))
         return "ldsReadModel 1 reads ldsAReadBytesPerCycle and ldsBTrReadBytesPerCycle, which must be positive";
     if (h.clockModel == 1 &&

@@ -334,6 +334,13 @@ def test_hardware_json_loader_is_all_or_nothing(tmp_path):
         (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 0x1p31'), "neither a number"),
         (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": inf'), "neither a number"),
         (good.read_text().replace('"clockHz": 2.1e9', '"clockHz": 2.e9'), "neither a number"),
+        # A term switch takes only the values the model defines.
+        (good.read_text().replace('"numSMs": 256', '"numSMs": 256, "labelModel": 3'),
+         "labelModel must be an integer from 0 to 2, found 3"),
+        (good.read_text().replace('"numSMs": 256', '"numSMs": 256, "launchModel": 2'),
+         "launchModel must be an integer from 0 to 1, found 2"),
+        (good.read_text().replace('"numSMs": 256', '"numSMs": 256, "l2ReuseModel": -1'),
+         "l2ReuseModel must be an integer from 0 to 2, found -1"),
     ]:
         broken = tmp_path / "broken.json"
         broken.write_text(text)
