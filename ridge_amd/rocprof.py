@@ -82,9 +82,11 @@ def short_name(name):
         parts = []
         while i < len(s) and s[i].isdigit():
             j = i
-            while s[j].isdigit():
+            while j < len(s) and s[j].isdigit():
                 j += 1
             n = int(s[i:j])
+            if j + n > len(s):
+                break
             parts.append(s[j:j + n])
             i = j + n
         if parts:
@@ -92,7 +94,9 @@ def short_name(name):
     for sep in ("<", "("):
         if sep in s:
             s = s[:s.index(sep)]
-    return s.split("::")[-1].strip() or name
+    # A demangled name may carry its return type ("void ns::kernel").
+    words = s.split("::")[-1].split()
+    return words[-1] if words else name
 
 
 def phases(parsed, min_run=1):

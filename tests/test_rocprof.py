@@ -28,7 +28,11 @@ def _write_counters(path, rows):
 def test_short_names_mangled_and_demangled():
     assert R.short_name(OURS) == "gemmMfmaKernel"
     assert R.short_name(FILL) == "fillUniformKernel"
-    assert R.short_name("void gemmMfmaPingPongKernel<256, 256, 32>(half const*)") == "void gemmMfmaPingPongKernel"
+    assert R.short_name("void gemmMfmaPingPongKernel<256, 256, 32>(half const*)") == "gemmMfmaPingPongKernel"
+    assert R.short_name("void ridge::gemmMfmaKernel<64, 64>(half const*)") == "gemmMfmaKernel"
+    # Truncated mangled names do not index past their end.
+    assert R.short_name("_Z3") == "_Z3"
+    assert R.short_name("_Z10abc") == "_Z10abc"
     assert R.short_name("Cijk_Ailk_Bljk_HHS_BH_MT256x256x64") == "Cijk_Ailk_Bljk_HHS_BH_MT256x256x64"
 
 
