@@ -371,9 +371,10 @@ def load_configs(path=CONFIGS_CSV):
 
 
 def cmd_run(args):
-    """The launches rocprofv3 observes: per config, LAUNCHES launches of the
-    registered variant, each followed by a synchronize; with a long factor F,
-    LAUNCHES more at K x F (the steady-state reference of the ENVELOPE rule)."""
+    """The launches rocprofv3 observes: per config and per K multiplier of its
+    registration (`Registration.factors`, the multiplier 1 first), LAUNCHES
+    launches of the registered variant at that K, each followed by a
+    synchronize."""
     import torch
     from ridge_amd import gemm as G
     reg = REGISTRATIONS[args.registration]
@@ -447,13 +448,6 @@ def gemm_dispatches(parsed, configs, launches):
     return groups
 
 
-def _counter(dispatch, name, xcds, grbm):
-    # GRBM_* clock counts are per XCD (rocprof.counter_value); every other
-    # counter of a dispatch is summed over its instances.
-    del grbm
-    return counter_value(dispatch, name, xcds)
-
-
 def cmd_gather(args):
     reg = REGISTRATIONS[args.registration]
     configs = load_configs(args.configs or reg.configs)
@@ -478,9 +472,11 @@ def cmd_gather(args):
         med = lambda xs: statistics.median(xs)  # noqa: E731
         row = {k: c[k] for k in cols}
         for name in PASS1_COUNTERS:
-            row[name] = med([_counter(d, name, xcds, name.startswith("GRBM_")) for d in p1[i][:n]])
-        row["FETCH_SIZE"] = med([_counter(d, "FETCH_SIZE", xcds, False) for d in pf[i][:n]])
-        row["WRITE_SIZE"] = med([_counter(d, "WRITE_SIZE", xcds, False) for d in pw[i][:n]])
+            # GRBM_* clock counts per XCD, every other counter summed over its
+            # instances (rocprof.counter_value).
+            row[name] = med([counter_value(d, name, xcds) for d in p1[i][:n]])
+        row["FETCH_SIZE"] = med([counter_value(d, "FETCH_SIZE", xcds) for d in pf[i][:n]])
+        row["WRITE_SIZE"] = med([counter_value(d, "WRITE_SIZE", xcds) for d in pw[i][:n]])
         for col in dcols:
             row[col] = ""
         for j, f in enumerate(facs[i]):

@@ -115,7 +115,7 @@ def test_gather_groups_dispatches_by_order_and_checks_names(tmp_path):
     groups = LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), configs, 2)
     assert [len(g) for g in groups] == [2, 2]
     # eight per-XCD rows: the max is the per-XCD count
-    assert LC._counter(groups[1][0], "GRBM_GUI_ACTIVE", 8, True) == 400.0
+    assert LC.counter_value(groups[1][0], "GRBM_GUI_ACTIVE", 8) == 400.0
     bad = [dict(configs[0]), dict(configs[1], groupM=4)]
     with pytest.raises(SystemExit, match="expected"):
         LC.gemm_dispatches(LC.parse_counter_dir(str(tmp_path / "p")), bad, 2)
