@@ -273,6 +273,7 @@ def test_random_divisible_shapes_uniform_inputs_every_variant(M, N, K):
     ref = O.gemm_f64(Arows, Bb, len(rows), N, K)
     absprod = O.gemm_f64(O.abs_bits(Arows), O.abs_bits(Bb), len(rows), N, K)
     max_a, max_b = _max_abs(Ab), _max_abs(Bb)
+    worst_row = (0.0, 0.0, "")
     for v in G.variants():
         assert v.divides(M, N, K)
         got = O.f16_bits_to_f32(_bits(_run(v.index, A, B, M, N, K))).reshape(M, N)[rows]
@@ -281,6 +282,9 @@ def test_random_divisible_shapes_uniform_inputs_every_variant(M, N, K):
         ok, frob, worst = O.passes_fp16(got, ref, absprod, K)
         assert ok, "%s on %dx%dx%d: FP16-output gate frob %.3e, worst element at %.2f of its bound" % (
             v.label(), M, N, K, frob, worst)
+        worst_row = max(worst_row, (worst, frob, v.label()))
+    print("  uniform %dx%dx%d, %d rows checked: worst element at %.3f of its bound (%s), frob %.3e" % (
+        M, N, K, len(rows), worst_row[0], worst_row[2], worst_row[1]), flush=True)
 
 
 def _persistent_edge_shapes(v):
