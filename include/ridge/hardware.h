@@ -109,7 +109,14 @@ struct HardwareModel {
                                      //    skeleton's row (128x128x64 w64x64 s4 with one compute wave
                                      //    per SIMD, 256x128x32 w64x64 s6 with two)
     double persistentStepCycles[2] = {0.0, 0.0};  // [CAL] cycles per K tile of those two skeletons
-    int mallReuseModel = 0;          // 0: every A/B byte an XCD's L2 misses is read from HBM (reference:
+    int persistentTileModel = 0;     // 0: a persistent walk's tiles pay no cost between them (each tile's
+                                     //    stores drain under the next body)
+                                     // 1: every tile a persistent workgroup walks adds, to its body, the
+                                     //    epilogue its compute waves run before the next tile (staging
+                                     //    through LDS, issuing the stores): the cycles the persistent
+                                     //    skeleton of the row's class measures per output tile
+    double persistentTileCycles[2] = {0.0, 0.0};  // [CAL] those cycles, one and two compute waves per SIMD
+    int mallReuseModel = 0;         // 0: every A/B byte an XCD's L2 misses is read from HBM (reference:
                                      //    one cache level)
                                      // 1: when A and B fit in the MALL (mallBytes), HBM supplies each
                                      //    once and the L2s' further misses (other XCDs re-fetching the

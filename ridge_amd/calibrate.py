@@ -117,6 +117,13 @@ def band_check(res, spec):
             # the ping-pong skeleton's K-step, and at best hide their reads.
             ok &= check(key, res[key], 0.45 * res["pingPongMfmaCycles"], 2.0 * res["pingPongMfmaCycles"], "cycles",
                         "persistent skeleton K tile: at least its MFMAs")
+    for i in (1, 2):
+        key, step = "persistentTileCycles%d" % i, "persistentStepCycles%d" % i
+        if key in res and step in res:
+            # Staging one output tile through LDS and issuing its stores: not
+            # negative, and a few K tiles at most.
+            ok &= check(key, res[key], 0.0, 8.0 * res[step], "cycles",
+                        "the epilogue between two output tiles of the persistent skeleton")
     if "mallRefillBytesPerSec" in res:
         ok &= check("mallRefillBytesPerSec", res["mallRefillBytesPerSec"] / 1e12, 1.0,
                     res["l2HitBytesPerCycle"] * res["clockHz"] / 1e12, "TB/s",
@@ -224,7 +231,8 @@ def hardware_json(res, spec, arch):
     # Constants of the later calibration benches, written (with the model term
     # that reads them switched on) when the log has them.
     for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec", "persistentStepCycles1",
-                 "persistentStepCycles2", "launchSeconds", "launchOverheadSeconds", "launchIsolatedSeconds"] +
+                 "persistentStepCycles2", "persistentTileCycles1", "persistentTileCycles2", "launchSeconds",
+                 "launchOverheadSeconds", "launchIsolatedSeconds"] +
                 ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
         if key in res:
             out[key] = res[key]
@@ -236,6 +244,8 @@ def hardware_json(res, spec, arch):
     for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]), ("fillLatencyModel", ["fillLatencySec"]),
                         ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)]),
                         ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"]),
+                        ("persistentTileModel", ["persistentStepCycles1", "persistentStepCycles2",
+                                                 "persistentTileCycles1", "persistentTileCycles2"]),
                         ("launchModel", ["launchOverheadSeconds"]),
                         ("labelModel", ["launchIsolatedSeconds", "hbmWriteBytesPerSec"])):
         if all(k in res for k in needs):

@@ -240,11 +240,19 @@ double pingPongCycles(int cus, const uint32_t* dOperands, const char* dRefill, c
 // k-step's reads, one barrier per K tile); the two loader waves refill the ring
 // with the kernel's direct-to-LDS loads and swizzled lane offsets, from a
 // four-tile L2-resident source. G K tiles per launch. Modes: 0 both halves of a
-// k-step, 1 the fragment reads alone, 2 the MFMAs alone (on fragments read once).
-// Every wave passes G barriers, as in the kernel.
+// k-step, 1 the fragment reads alone, 2 the MFMAs alone (on fragments read once),
+// 3 mode 0 with the kernel's epilogue after every tileK K tiles: the compute
+// waves stage their tile through their LDS region, store it non-temporally
+// (storeStaged, as the kernel does) and clear their accumulators. Workgroup b's
+// epilogues rotate over kEpiSlots output tiles of C, rows
+// [(b kEpiSlots + slot) BM, +BM), columns [0, BN): C holds
+// gridDim.x x kEpiSlots x BM rows of BN halves. Every wave passes G barriers,
+// as in the kernel.
+constexpr int kEpiSlots = 16;
+
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int Mode>
 __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders) * 64) void persistentSkeletonKernel(
-    const _Float16* src, int G, float* sink, Stamp* out) {
+    const _Float16* src, int G, float* sink, Stamp* out, _Float16* C, int tileK) {
     using T = ridge::GemmTraits<BM, BN, BK, WM, WN, STAGES, 8>;
     using P = ridge::PersistentTraits<BM, BN, BK, WM, WN, STAGES, 8>;
     using Blk = ridge::GemmBlock<BM, BN, BK, WM, WN, STAGES, 8>;
@@ -313,8 +321,11 @@ __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders)
         return;
     }
     // One column of tiles, one per workgroup: the block only forms its LDS
-    // fragment offsets here and never touches global memory.
-    Blk blk(lds, src, src, BM * (int)gridDim.x, BN, BK * G);
+    // fragment offsets here and reads no global memory; mode 3 writes C.
+    const int rowsC = BM * (int)gridDim.x * (Mode == 3 ? kEpiSlots : 1);
+    Blk blk(lds, src, src, rowsC, BN, BK * G);
+    RIDGE_LDS_AS char* region = (RIDGE_LDS_AS char*)(lds) + T::kLdsBytes + wave * P::kRegionBytes;
+    (void)region;
     ridge::barrierLds();  // B_0
     half8_t fa[2][TM];
     half8_t fb[2][TN];
@@ -348,6 +359,20 @@ __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders)
                         for (int tn = 0; tn < TN; ++tn) asm volatile("" ::"v"(fb[cur][tn]));
                     }
                 }
+                if constexpr (Mode == 3) {
+                    if ((g + 1) % tileK == 0) {
+                        const int slot = ((g + 1) / tileK) % kEpiSlots;
+                        blk.setTile((int)blockIdx.x * kEpiSlots + slot, rowsC, BN, BK * G);
+                        ridge::storeStaged<TM, TN, WN, P::kEpiTiles, true>(blk.acc, region, blk.waveC(C, BN), BN,
+                                                                           lane);
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                            for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) blk.acc[tm][tn][e] = 0.0f;
+                    }
+                }
             }
         });
     }
@@ -368,10 +393,12 @@ constexpr int kPersistentTiles = 1024;  // K tiles per skeleton launch
 // Median cycles per K tile of the persistent skeleton over every CU (one
 // workgroup each), and the median clock.
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int Mode>
-double persistentCycles(int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, double& clockHz) {
+double persistentCycles(int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, double& clockHz,
+                        _Float16* dC = nullptr, int tileK = 1) {
     using P = ridge::PersistentTraits<BM, BN, BK, WM, WN, STAGES, 8>;
     auto k = persistentSkeletonKernel<BM, BN, BK, WM, WN, STAGES, Mode>;
-    hipLaunchKernelGGL(k, dim3(cus), dim3(P::kThreads), 0, nullptr, dSrc, kPersistentTiles, dSink, dStamps);
+    hipLaunchKernelGGL(k, dim3(cus), dim3(P::kThreads), 0, nullptr, dSrc, kPersistentTiles, dSink, dStamps, dC,
+                       tileK);
     CAL_HIP_CHECK(hipGetLastError());
     CAL_HIP_CHECK(hipDeviceSynchronize());
     std::vector<Stamp> st(cus);
@@ -408,6 +435,42 @@ double persistentStep(const char* key, int cus, const _Float16* dSrc, float* dSi
     std::printf("CAL_INFO %sClockHz %.6e\n", key, hzBoth);
     std::printf("CAL_RESULT %s %.6f\n", key, tBoth);
     return tBoth;
+}
+
+// The epilogue a persistent row's compute waves run between two output tiles,
+// in cycles per tile: the skeleton with the epilogue after every tileK K tiles
+// against the same skeleton without it, (t(tileK) - t) x tileK, at tileK = 4, 8,
+// 16 and 32 K tiles per output tile, each launch pair alternated within a
+// repeat. Reported as `key`, the middle of the four; each tile length beside it
+// as a record (a constant cost per tile gives four equal figures).
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+double persistentTileCost(const char* key, int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, _Float16* dC,
+                          bool& ok) {
+    constexpr int kTileKs[4] = {4, 8, 16, 32};
+    std::vector<double> perLength[4];
+    for (int r = 0; r < kRepeats; ++r) {
+        for (int i = 0; i < 4; ++i) {
+            double hz = 0.0;
+            const double base = persistentCycles<BM, BN, BK, WM, WN, STAGES, 0>(cus, dSrc, dSink, dStamps, hz);
+            const double epi =
+                persistentCycles<BM, BN, BK, WM, WN, STAGES, 3>(cus, dSrc, dSink, dStamps, hz, dC, kTileKs[i]);
+            perLength[i].push_back((epi - base) * kTileKs[i]);
+        }
+    }
+    std::vector<double> estimates;
+    std::printf("  %dx%dx%d w%dx%d s%d: epilogue cycles per output tile at", BM, BN, BK, WM, WN, STAGES);
+    for (int i = 0; i < 4; ++i) {
+        estimates.push_back(middle(perLength[i]));
+        std::printf(" %d: %.0f%s", kTileKs[i], estimates.back(), i < 3 ? "," : "");
+    }
+    std::printf(" K tiles per tile\n");
+    for (int i = 0; i < 4; ++i) std::printf("CAL_INFO %sTileK%d %.6f\n", key, kTileKs[i], estimates[i]);
+    const double cost = middle(estimates);
+    // A difference of two timings, about a tenth of a K tile at tileK = 32, so
+    // the four tile lengths are held to half the cost of one another.
+    ok &= reportConstant(key, cost, "cycles", estimates, 0.50);
+    std::printf("CAL_RESULT %s %.6f\n", key, cost);
+    return cost;
 }
 
 // U[-1,1) halves from splitmix64, packed two per word: 16 KiB.
@@ -616,6 +679,15 @@ int main() {
                                 hipMemcpyHostToDevice));
     persistentStep<128, 128, 64, 64, 64, 4>("persistentStepCycles1", cus, dSrc, dFSink, dStamps, ok);
     persistentStep<256, 128, 32, 64, 64, 6>("persistentStepCycles2", cus, dSrc, dFSink, dStamps, ok);
+    // The epilogue between output tiles, for the same two rows. C: cus x
+    // kEpiSlots output tiles of the larger row (256 x 128 halves each).
+    std::printf("\npersistent skeleton with the kernel's epilogue between output tiles\n");
+    _Float16* dC = nullptr;
+    const size_t cBytes = size_t(cus) * kEpiSlots * 256 * 128 * sizeof(_Float16);
+    CAL_HIP_CHECK(hipMalloc(&dC, cBytes));
+    persistentTileCost<128, 128, 64, 64, 64, 4>("persistentTileCycles1", cus, dSrc, dFSink, dStamps, dC, ok);
+    persistentTileCost<256, 128, 32, 64, 64, 6>("persistentTileCycles2", cus, dSrc, dFSink, dStamps, dC, ok);
+    CAL_HIP_CHECK(hipFree(dC));
     CAL_HIP_CHECK(hipFree(dSrc));
     CAL_HIP_CHECK(hipFree(dOperands));
     CAL_HIP_CHECK(hipFree(dRefill));

@@ -120,6 +120,8 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("mallStretch1", h.mallStretch[1]), R("mallStretch2", h.mallStretch[2]), R("mallStretch3", h.mallStretch[3]),
         R("mallStretch4", h.mallStretch[4]), I("persistentStepModel", h.persistentStepModel),
         R("persistentStepCycles1", h.persistentStepCycles[0]), R("persistentStepCycles2", h.persistentStepCycles[1]),
+        I("persistentTileModel", h.persistentTileModel), R("persistentTileCycles1", h.persistentTileCycles[0]),
+        R("persistentTileCycles2", h.persistentTileCycles[1]),
         I("fillShareModel", h.fillShareModel), I("mallReuseModel", h.mallReuseModel), R("mallBytes", h.mallBytes),
         I("launchModel", h.launchModel), R("launchOverheadSeconds", h.launchOverheadSeconds),
         R("launchIsolatedSeconds", h.launchIsolatedSeconds), I("labelModel", h.labelModel),
@@ -173,7 +175,8 @@ std::string inconsistency(const HardwareModel& h) {
         {"l2StreamModel", h.l2StreamModel, 1},   {"uniformOverlapModel", h.uniformOverlapModel, 1},
         {"powerModel", h.powerModel, 1},         {"hbmWriteModel", h.hbmWriteModel, 1},
         {"fillLatencyModel", h.fillLatencyModel, 1}, {"mallStreamModel", h.mallStreamModel, 1},
-        {"persistentStepModel", h.persistentStepModel, 1}, {"fillShareModel", h.fillShareModel, 1},
+        {"persistentStepModel", h.persistentStepModel, 1}, {"persistentTileModel", h.persistentTileModel, 1},
+        {"fillShareModel", h.fillShareModel, 1},
         {"mallReuseModel", h.mallReuseModel, 1}, {"launchModel", h.launchModel, 1},
         {"labelModel", h.labelModel, 2},
     };
@@ -210,6 +213,10 @@ std::string inconsistency(const HardwareModel& h) {
         return "mallReuseModel 1 reads mallRefillBytesPerSec and mallBytes, which must be positive";
     if (h.persistentStepModel == 1 && !(h.persistentStepCycles[0] > 0.0 && h.persistentStepCycles[1] > 0.0))
         return "persistentStepModel 1 reads persistentStepCycles1 and persistentStepCycles2, which must be positive";
+    if (h.persistentTileModel == 1 && !(h.persistentTileCycles[0] >= 0.0 && h.persistentTileCycles[1] >= 0.0 &&
+                                        h.persistentModel == 1 && h.persistentStepModel == 1))
+        return "persistentTileModel 1 reads persistentTileCycles1 and persistentTileCycles2 (not negative; cycles "
+               "of the persistent skeletons) and needs persistentModel 1 and persistentStepModel 1";
     if (h.launchModel == 1 && !(h.launchOverheadSeconds >= 0.0))
         return "launchModel 1 reads launchOverheadSeconds, which must not be negative";
     if (h.labelModel == 1 && !(h.launchIsolatedSeconds >= 0.0 && h.hbmWriteModel == 1 && h.simdsPerSM > 0))

@@ -64,6 +64,10 @@
 //                           MFMAs scaled by the measured/modelled ratio of the
 //                           persistent skeleton of its class (one or two compute
 //                           waves per SIMD) (reference: no persistent rows)
+//   persistent tiles      = hw.persistentTileModel 1: every tile a persistent
+//                           workgroup walks adds the epilogue its compute waves
+//                           run before the next one, as the same skeleton with
+//                           the kernel's epilogue measures it per output tile
 //   persistent rows       = hw.persistentModel 1 and cfg.schedule 2: two loader
 //                           waves and the epilogue staging join the workgroup,
 //                           which walks ceil(tiles / slots) tiles and pays one
@@ -420,7 +424,13 @@ Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
         // tiles: one fill, that many bodies (each tile's stores drain under the
         // next body), one drain.
         const double walked = tBody * fullWaves;
-        envelopeEfficiency = walked / (tPrologue + walked + tEpilogue);
+        // persistentTileModel 1: before each next tile the compute waves stage
+        // the finished tile through LDS and issue its stores, with no MFMA to
+        // run; the skeleton of the row's class measures those cycles per tile.
+        double between = 0.0;
+        if (hw.persistentTileModel == 1 && hw.simdsPerSM > 0)
+            between = fullWaves * hw.persistentTileCycles[numWarps / hw.simdsPerSM >= 2 ? 1 : 0];
+        envelopeEfficiency = walked / (tPrologue + walked + between + tEpilogue);
     } else {
         envelopeEfficiency = tBody / (tPrologue + tBody + tEpilogue);
     }

@@ -731,6 +731,49 @@ def test_persistent_step_model_scales_by_the_skeleton_of_the_class(tmp_path):
         RM.Hardware(str(bad))
 
 
+def test_persistent_tile_model_charges_the_epilogue_between_tiles(tmp_path):
+    """persistentTileModel 1 on the placeholders, with skeleton K tiles equal to the
+    rows' own reads + MFMAs (1024 cycles each, so the step ratio is 1) and
+    measured epilogues of 1000 cycles per tile (one compute wave per SIMD) and 500
+    (two). At 8192 x 8192 x 128:
+
+      128x128x64 w64x64 s4 (4 compute waves): 16 tiles per slot, body 2 x 1024,
+        prologue 2 x 32768 B / 13.0208333 = 5033.1648, drain 2516.5824;
+        envelope 32768 / (5033.1648 + 32768 + 16 x 1000 + 2516.5824) = 0.581841
+        (without the term 32768 / 40317.7472 = 0.812744);
+      256x128x32 w64x64 s6 (8 compute waves): 8 tiles per slot, body 4 x 1024,
+        prologue 4 x 24576 B / 13.0208333 = 7549.7472, drain 5033.1648;
+        envelope 32768 / (7549.7472 + 32768 + 8 x 500 + 5033.1648) = 0.663980.
+
+    One-tile-per-workgroup rows pay nothing; the term needs the step term."""
+    base = ', "persistentStepModel": 1, "persistentStepCycles1": 1024, "persistentStepCycles2": 1024'
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % (base + ', "persistentTileModel": 1, "persistentTileCycles1": 1000, '
+                                        '"persistentTileCycles2": 500'))
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % base)
+    hw_on, hw_off = RM.Hardware(str(on)), RM.Hardware(str(off))
+    four = dict(M=8192, N=8192, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=4, regsPerThread=185,
+                groupM=8, schedule=2)
+    assert RM.predict(hw_off, **four)["envelopeEfficiency"] == pytest.approx(32768 / 40317.7472, abs=1e-9)
+    p4 = RM.predict(hw_on, **four)
+    assert p4["tStepCycles"] == pytest.approx(1024.0) and p4["wavesExact"] == pytest.approx(16.0)
+    assert p4["envelopeEfficiency"] == pytest.approx(32768 / (5033.1648 + 32768 + 16000 + 2516.5824), abs=1e-9)
+    eight = dict(four, BM=256, BK=32, stages=6, regsPerThread=167, groupM=4)
+    p8 = RM.predict(hw_on, **eight)
+    assert p8["tStepCycles"] == pytest.approx(1024.0) and p8["wavesExact"] == pytest.approx(8.0)
+    assert p8["tPrologueCycles"] == pytest.approx(7549.7472, abs=1e-3)
+    assert p8["tEpilogueCycles"] == pytest.approx(5033.1648, abs=1e-3)
+    assert p8["envelopeEfficiency"] == pytest.approx(32768 / (7549.7472 + 32768 + 4000 + 5033.1648), abs=1e-9)
+    uniform = dict(four, schedule=0)
+    assert RM.predict(hw_on, **uniform) == RM.predict(hw_off, **uniform)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "persistentTileModel": 1, "persistentTileCycles1": 1000, '
+                                 '"persistentTileCycles2": 500')
+    with pytest.raises(ValueError, match="persistentTileModel 1"):
+        RM.Hardware(str(bad))
+
+
 def test_fill_share_model_fetches_each_panel_slice_once_per_xcd(tmp_path):
     """fillShareModel 1 with HBM at 8 TB/s and the L2s at 8192 B/cycle x 2.4 GHz
     = 19.6608 TB/s, on one XCD. 2048 x 2048 x 1024 on 128x128x64 w64x64 s2: two
