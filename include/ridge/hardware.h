@@ -114,7 +114,9 @@ struct HardwareModel {
                                      // 1: every tile a persistent workgroup walks adds, to its body, the
                                      //    epilogue its compute waves run before the next tile (staging
                                      //    through LDS, issuing the stores): the cycles the persistent
-                                     //    skeleton of the row's class measures per output tile
+                                     //    skeleton of the row's class measures per output tile.
+                                     //    The calibration writes the cycles but leaves the term off:
+                                     //    with them it predicts worse on the measured sweeps
     double persistentTileCycles[2] = {0.0, 0.0};  // [CAL] those cycles, one and two compute waves per SIMD
     int mallReuseModel = 0;         // 0: every A/B byte an XCD's L2 misses is read from HBM (reference:
                                      //    one cache level)

@@ -326,6 +326,11 @@ __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders)
     Blk blk(lds, src, src, rowsC, BN, BK * G);
     RIDGE_LDS_AS char* region = (RIDGE_LDS_AS char*)(lds) + T::kLdsBytes + wave * P::kRegionBytes;
     (void)region;
+    // The kernel's own tile cursor: a K-tile count compared with K / BK, and the
+    // tile index, so the loop carries the same per-K-tile work as the kernel's.
+    int kt = 0, tile = 0;
+    (void)kt;
+    (void)tile;
     ridge::barrierLds();  // B_0
     half8_t fa[2][TM];
     half8_t fb[2][TN];
@@ -360,9 +365,8 @@ __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders)
                     }
                 }
                 if constexpr (Mode == 3) {
-                    if ((g + 1) % tileK == 0) {
-                        const int slot = ((g + 1) / tileK) % kEpiSlots;
-                        blk.setTile((int)blockIdx.x * kEpiSlots + slot, rowsC, BN, BK * G);
+                    if (++kt == tileK) {
+                        blk.setTile((int)blockIdx.x * kEpiSlots + (tile % kEpiSlots), rowsC, BN, BK * G);
                         ridge::storeStaged<TM, TN, WN, P::kEpiTiles, true>(blk.acc, region, blk.waveC(C, BN), BN,
                                                                            lane);
 #pragma unroll
@@ -371,6 +375,8 @@ __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders)
                             for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) blk.acc[tm][tn][e] = 0.0f;
+                        kt = 0;
+                        ++tile;
                     }
                 }
             }

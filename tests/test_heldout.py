@@ -374,3 +374,35 @@ def test_best_row_against_hipblaslt_on_every_sweep_shape():
     assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.135, abs=0.001)
     assert min(ratios)[1] == (8192, 16384, 4096) and max(ratios)[1] == (1024, 1024, 128)
     assert min(xs) == pytest.approx(1.029, abs=0.001) and max(xs) == pytest.approx(1.843, abs=0.001)
+
+
+def test_persistent_tile_term_was_measured_and_is_not_adopted():
+    """persistentTileModel with the per-tile epilogue cycles cal-smem-bw measured
+    (data/hardware/mi355x-calibration-tile-epilogue.txt) on top of the committed
+    calibration: MAPE and regret at k = 1 rise in sample (9.89 -> 10.88%, 1.19 ->
+    2.14%) and held-out 1's worst shape worsens (11.04 -> 17.13%), though
+    held-out 5's improves (12.23 -> 7.10%). The committed model keeps it off."""
+    import json
+    from ridge_amd import calibrate as C
+    with_term = os.path.join(ROOT, "data", "hardware", "mi355x-tile-epilogue.json")
+    log = os.path.join(ROOT, "data", "hardware", "mi355x-calibration-tile-epilogue.txt")
+    measured = C.parse_results(open(log).read())
+    h, t = json.load(open(CURRENT_HW)), json.load(open(with_term))
+    assert h.get("persistentTileModel", 0) == 0
+    assert t["persistentTileModel"] == 1
+    for i in (1, 2):
+        key = "persistentTileCycles%d" % i
+        assert t[key] == pytest.approx(measured[key], abs=1e-6)
+        # The skeleton K tiles of that run equal the committed calibration's.
+        assert measured["persistentStepCycles%d" % i] == pytest.approx(h["persistentStepCycles%d" % i], rel=1e-5)
+    assert {k: v for k, v in t.items() if not k.startswith("persistentTile") and k != "note"} == \
+        {k: v for k, v in h.items() if k != "note"}
+    figures = {}
+    for name in ("mi355x.csv", "mi355x-heldout.csv", "mi355x-heldout5.csv"):
+        path = os.path.join(ROOT, "data", "measured", name)
+        rows = V.join(path, with_term)
+        result, _, _, _ = AT.evaluate(path, with_term, ks=(1,))
+        figures[name] = (sum(j.abs_pct for j in rows) / len(rows), result[0]["mean_regret"], result[0]["max_regret"])
+    assert figures["mi355x.csv"] == pytest.approx((10.88, 2.14, 9.15), abs=0.01)
+    assert figures["mi355x-heldout.csv"][2] == pytest.approx(17.13, abs=0.01)
+    assert figures["mi355x-heldout5.csv"][2] == pytest.approx(7.10, abs=0.01)
