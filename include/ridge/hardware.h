@@ -88,6 +88,12 @@ struct HardwareModel {
                                      //    time, so the two times add (the epilogue drains at the
                                      //    write rate too)
     double hbmWriteBytesPerSec = 0.0;  // [CAL] streaming 16-byte stores, whole GPU (cal-hbm-bw)
+    int writeOverlapModel = 0;       // 0: DRAM reads, DRAM writes and (l2StreamModel 1) L2-served
+                                     //    loads take the sum of their times
+                                     // 1: two resources, each used in series: the DRAM bus (reads,
+                                     //    then writes) and the CUs' load path (DRAM-served loads, then
+                                     //    L2-served ones); the writes and the L2-served loads overlap,
+                                     //    so the time is reads + max(writes, L2-served loads)
     int fillLatencyModel = 0;        // 0: fill costs only its bytes at the DRAM rate (reference)
                                      // 1: each round of one-tile-per-workgroup workgroups (one
                                      //    round in all for a persistent grid) also waits

@@ -241,7 +241,11 @@ def hardware_json(res, spec, arch):
         # is the calibrated refill path's.
         out["mallBytes"] = spec["mall_bytes"]
         out["mallReuseModel"] = 1
-    for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]), ("fillLatencyModel", ["fillLatencySec"]),
+    for term, needs in (("hbmWriteModel", ["hbmWriteBytesPerSec"]),
+                        # No constant of its own: it overlaps the write stream with
+                        # the L2-served loads (l2StreamModel is always on here).
+                        ("writeOverlapModel", ["hbmWriteBytesPerSec"]),
+                        ("fillLatencyModel", ["fillLatencySec"]),
                         ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)]),
                         ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"]),
                         ("launchModel", ["launchOverheadSeconds"]),

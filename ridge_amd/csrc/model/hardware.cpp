@@ -112,6 +112,7 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("freeRunningOverlap", h.freeRunningOverlap), I("powerModel", h.powerModel),
         R("loadedClockRatio", h.loadedClockRatio), R("warpsNeededToHideIlp8", h.warpsNeededToHideIlp8),
         I("hbmWriteModel", h.hbmWriteModel), R("hbmWriteBytesPerSec", h.hbmWriteBytesPerSec),
+        I("writeOverlapModel", h.writeOverlapModel),
         I("fillLatencyModel", h.fillLatencyModel), R("fillLatencySec", h.fillLatencySec),
         I("mallStreamModel", h.mallStreamModel), R("mallRefillBytesPerSec", h.mallRefillBytesPerSec),
         R("mallStretchLoad0", h.mallStretchLoad[0]), R("mallStretchLoad1", h.mallStretchLoad[1]),
@@ -174,6 +175,7 @@ std::string inconsistency(const HardwareModel& h) {
         {"ldsReadModel", h.ldsReadModel, 1},     {"clockModel", h.clockModel, 1},
         {"l2StreamModel", h.l2StreamModel, 1},   {"uniformOverlapModel", h.uniformOverlapModel, 1},
         {"powerModel", h.powerModel, 1},         {"hbmWriteModel", h.hbmWriteModel, 1},
+        {"writeOverlapModel", h.writeOverlapModel, 1},
         {"fillLatencyModel", h.fillLatencyModel, 1}, {"mallStreamModel", h.mallStreamModel, 1},
         {"persistentStepModel", h.persistentStepModel, 1}, {"persistentTileModel", h.persistentTileModel, 1},
         {"fillShareModel", h.fillShareModel, 1},
@@ -205,6 +207,9 @@ std::string inconsistency(const HardwareModel& h) {
     }
     if (h.hbmWriteModel == 1 && !(h.hbmWriteBytesPerSec > 0.0))
         return "hbmWriteModel 1 reads hbmWriteBytesPerSec, which must be positive";
+    if (h.writeOverlapModel == 1 && !(h.hbmWriteModel == 1 && h.l2StreamModel == 1))
+        return "writeOverlapModel 1 overlaps hbmWriteModel's writes with l2StreamModel's L2-served loads, and "
+               "needs both switched on";
     if (h.fillLatencyModel == 1 && !(h.fillLatencySec > 0.0))
         return "fillLatencyModel 1 reads fillLatencySec, which must be positive";
     if (h.fillShareModel == 1 && !(h.l2HitBytesPerCycle > 0.0))

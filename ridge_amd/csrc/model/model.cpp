@@ -64,6 +64,9 @@
 //                           MFMAs scaled by the measured/modelled ratio of the
 //                           persistent skeleton of its class (one or two compute
 //                           waves per SIMD) (reference: no persistent rows)
+//   write overlap         = hw.writeOverlapModel 1: C's writes to DRAM overlap
+//                           the tile loads the L2s serve; the DRAM reads come
+//                           before both (reference: one DRAM stream)
 //   persistent tiles      = hw.persistentTileModel 1: every tile a persistent
 //                           workgroup walks adds the epilogue its compute waves
 //                           run before the next one, as the same skeleton with
@@ -528,18 +531,26 @@ Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
         const double writeBytes = M * N * hw.cBytes;
         p.dramReadBytes = readBytes;
         p.dramWriteBytes = writeBytes;
-        double seconds = readBytes / hw.hbmBytesPerSec + writeBytes / hw.hbmWriteBytesPerSec;
+        double readSeconds = readBytes / hw.hbmBytesPerSec;
         if (hw.mallReuseModel == 1 && (M * K + K * N) * db <= hw.mallBytes) {
             // A and B stay in the MALL: HBM supplies each byte once, and the
             // L2s' further misses (XCDs re-fetching panels) are MALL hits.
             const double compulsory = (M * K + K * N) * db;
-            seconds = compulsory / hw.hbmBytesPerSec + (readBytes - compulsory) / hw.mallRefillBytesPerSec +
-                      writeBytes / hw.hbmWriteBytesPerSec;
+            readSeconds = compulsory / hw.hbmBytesPerSec + (readBytes - compulsory) / hw.mallRefillBytesPerSec;
         }
+        const double writeSeconds = writeBytes / hw.hbmWriteBytesPerSec;
+        double l2Seconds = 0.0;
         if (hw.l2StreamModel == 1) {
             p.l2HitBytes = std::max(0.0, flops / baseIntensity - readBytes);
-            seconds += p.l2HitBytes / (hw.l2HitBytesPerCycle * hw.clockHz);
+            l2Seconds = p.l2HitBytes / (hw.l2HitBytesPerCycle * hw.clockHz);
         }
+        // writeOverlapModel 1: two resources, each used in series. The DRAM bus
+        // carries the reads, then the writes; the CUs' load path takes the loads
+        // DRAM serves, then the ones the L2s serve. C's writes and the L2-served
+        // loads use neither in common, so they overlap, and the busier resource
+        // bounds the launch. Otherwise the three streams are summed.
+        const double seconds = hw.writeOverlapModel == 1 ? readSeconds + std::max(writeSeconds, l2Seconds)
+                                                         : readSeconds + writeSeconds + l2Seconds;
         p.arithmeticIntensity = flops / (readBytes + writeBytes);
         p.hbmTFLOPS = flops / seconds / 1e12;
     } else if (hw.l2StreamModel == 1) {

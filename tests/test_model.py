@@ -640,6 +640,36 @@ def test_hbm_write_model_prices_c_at_the_write_rate(tmp_path):
     assert p_on["tEpilogueCycles"] == pytest.approx(2 * p_off["tEpilogueCycles"])
 
 
+def test_write_overlap_model_overlaps_c_with_the_l2_served_loads(tmp_path):
+    """writeOverlapModel 1 on the case above plus l2StreamModel 1: the 256 tiles
+    load (128 + 128) x 128 x 2 B each, 16,777,216 B, of which 1,048,576 come from
+    DRAM and 15,728,640 from the L2s. At 4096 B/cycle x 2.4 GHz the L2-served
+    loads take 1.6 us; in series with the reads (0.131072 us) and the writes
+    (2.097152 us) the launch takes 3.828224 us, 280.479 TFLOP/s. With the term the
+    writes overlap them: 0.131072 + max(2.097152, 1.6) = 2.228224 us, 481.882. At
+    2048 B/cycle the L2-served loads take 3.2 us and bind instead: 0.131072 + 3.2 =
+    3.331072 us. The term needs both stream terms."""
+    base = ', "numXcds": 1, "hbmWriteModel": 1, "hbmWriteBytesPerSec": 4e12, "l2StreamModel": 1'
+    cfg = dict(M=2048, N=2048, K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128)
+    flops = 2.0 * 2048 * 2048 * 128
+    pred = {}
+    for name, extra in (("series", ', "l2HitBytesPerCycle": 4096'),
+                        ("overlap", ', "l2HitBytesPerCycle": 4096, "writeOverlapModel": 1'),
+                        ("l2bound", ', "l2HitBytesPerCycle": 2048, "writeOverlapModel": 1')):
+        f = tmp_path / (name + ".json")
+        f.write_text(_CDNA4_JSON % (base + extra))
+        pred[name] = RM.predict(RM.Hardware(str(f)), **cfg)
+    assert pred["series"]["l2HitBytes"] == pytest.approx(15728640.0)
+    assert pred["series"]["hbmTFLOPS"] == pytest.approx(flops / 3.828224e-6 / 1e12)
+    assert pred["overlap"]["hbmTFLOPS"] == pytest.approx(flops / 2.228224e-6 / 1e12)
+    assert pred["overlap"]["hbmTFLOPS"] == pytest.approx(481.882, abs=1e-3)
+    assert pred["l2bound"]["hbmTFLOPS"] == pytest.approx(flops / 3.331072e-6 / 1e12)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "numXcds": 1, "writeOverlapModel": 1')
+    with pytest.raises(ValueError, match="writeOverlapModel 1"):
+        RM.Hardware(str(bad))
+
+
 def test_mall_reuse_model_serves_refetches_from_the_mall(tmp_path):
     """mallReuseModel 1 with reads at 8 TB/s, writes at 4 TB/s and MALL hits at
     2 TB/s, 8 XCDs in the launch order (l2ReuseModel 2): the 256 resident 128x128
