@@ -422,3 +422,24 @@ def test_persistent_tile_term_was_measured_and_is_not_adopted():
     assert figures["mi355x.csv"] == pytest.approx((10.38, 2.84, 17.85), abs=0.01)
     assert figures["mi355x-heldout.csv"][2] == pytest.approx(20.55, abs=0.01)
     assert figures["mi355x-heldout5.csv"][2] == pytest.approx(13.36, abs=0.01)
+
+
+def test_sweep_draw_refuses_an_exhausted_space_and_reproduces_the_committed_files(tmp_path):
+    """The 100 shapes of the registered value sets are all taken by the in-sample
+    sweep, the six held-out sweeps and the BASELINE configs: a seventh draw from
+    them is refused instead of redrawing forever. Sets that some table row would
+    not divide are refused. The generator still writes the committed files."""
+    from ridge_amd import sweep as S
+    taken = []
+    for path in [IN_SAMPLE, BASELINE_SHAPES] + [os.path.join(ROOT, "data", "sweep", "mi355x-heldout%s-registered.csv" % s)
+                                                for s in ("", "2", "3", "4", "5", "6")]:
+        taken += [s[:3] for s in T.read_shapes(path)]
+    with pytest.raises(ValueError, match="holds 0 shapes"):
+        S.registered_shapes(0x1234, exclude=taken)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        S.registered_shapes(0x1234, mn_choices=(1024, 1280 + 64))
+    with pytest.raises(ValueError, match="every K of 128"):
+        S.registered_shapes(0x1234, k_choices=(64, 128))
+    out = tmp_path / "s.csv"
+    S.main(["--out", str(out), "--baseline-out", "-"])
+    assert out.read_text() == open(IN_SAMPLE).read()
