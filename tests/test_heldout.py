@@ -443,3 +443,31 @@ def test_sweep_draw_refuses_an_exhausted_space_and_reproduces_the_committed_file
     out = tmp_path / "s.csv"
     S.main(["--out", str(out), "--baseline-out", "-"])
     assert out.read_text() == open(IN_SAMPLE).read()
+
+
+# The seventh held-out sweep (data/sweep/mi355x-heldout7.md).
+REGISTERED7 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout7-registered.csv")
+FROZEN7 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout7-hw.json")
+TABLE7 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout7-table.csv")
+
+
+def test_seventh_heldout_registration():
+    """14 shapes from the new value sets, none in an earlier set; the sixth set's
+    table; the sixth set's constants with writeOverlapModel 1 and nothing else
+    changed."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED7)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, REGISTERED6,
+                 BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    assert len(held) == 14 and not held & earlier
+    assert all(M in (1536, 3072, 5120, 6144, 12288) and N in (1536, 3072, 5120, 6144, 12288) and
+               K in (256, 2048, 3072, 6144) for M, N, K in held)
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE7) == keys(TABLE6) == list(V.kernel_table_keys())
+    six, seven = json.load(open(FROZEN6)), json.load(open(FROZEN7))
+    assert seven["writeOverlapModel"] == 1 and "writeOverlapModel" not in six
+    assert {k: v for k, v in seven.items() if k != "writeOverlapModel"} == six
+    assert seven.get("persistentTileModel", 0) == 0
