@@ -114,6 +114,27 @@ int ridge_blaslt_prepare(void* handle, const void* A, const void* B, void* C, in
 int ridge_blaslt_gemm(void* handle, const void* A, const void* B, void* C, int M, int N, int K, int c_is_f32,
                       void* stream);
 
+/* Row split: a grid whose tiles fill whole rounds of resident workgroups and then
+ * a fraction of one more (wave quantisation, e.g. 288 tiles of 256 x 256 on 256
+ * CUs) runs the whole rounds with one row on the first rows of C and the rest of
+ * the rows with another, usually smaller-tile, row. No counterpart in the
+ * reference, whose callers launch one variant per shape; these two calls sit
+ * beside that contract and change nothing in it.
+ *
+ * ridge_gemm_split_rows: rows of C the body row `body` takes, the largest multiple
+ *   of its BM whose tiles fill whole rounds of its resident workgroups on numCUs
+ *   CUs (workgroups per CU from its LDS bytes, waves and the compiler's waves per
+ *   SIMD). Returns M when the grid is already whole rounds, 0 when it is less than
+ *   one round, -1 for a bad index, CU count or a shape the row does not divide.
+ * ridge_gemm_launch_split: variant `body` on rows [0, bodyRows) of A and C and
+ *   variant `tail` on rows [bodyRows, M), back to back on `stream`. Both sub-shapes
+ *   must be ones their variants divide and 0 < bodyRows < M; every check is made
+ *   before the first launch, so a refused call (1, hipErrorInvalidValue) enqueues
+ *   nothing. Returns the first launch error otherwise. */
+int ridge_gemm_split_rows(int body, int M, int N, int K, int numCUs);
+int ridge_gemm_launch_split(int body, int tail, int bodyRows, const void* A, const void* B, void* C, int M, int N,
+                            int K, void* stream);
+
 /* Library identification for logs: "ridge_gemm gfx950 <build info>". */
 const char* ridge_gemm_build_info(void);
 

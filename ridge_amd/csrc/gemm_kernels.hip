@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -175,6 +176,39 @@ int ridge_gemm_launch(int i, const void* A, const void* B, void* C, int M, int N
     if (A == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
     if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15u) return (int)hipErrorInvalidValue;
     return (int)kTable[i].launch(A, B, C, M, N, K, static_cast<hipStream_t>(stream));
+}
+
+int ridge_gemm_split_rows(int body, int M, int N, int K, int numCUs) {
+    if (!validIndex(body) || numCUs <= 0 || !ridge_gemm_divides(body, M, N, K)) return -1;
+    ridge_gemm_variant_t v;
+    ridge_gemm_get_variant(body, &v);
+    // Resident workgroups per CU: LDS, wave slots, and the register file (the
+    // compiler's waves per SIMD; a workgroup's waves spread over the 4 SIMDs).
+    int perCU = 163840 / v.ldsBytes;
+    perCU = std::min(perCU, 32 / v.waves);
+    if (v.occupancy > 0) perCU = std::min(perCU, v.occupancy / ((v.waves + 3) / 4));
+    if (perCU < 1) return -1;
+    const long long slots = (long long)perCU * numCUs;
+    const long long perPanel = N / v.BN, panels = M / v.BM;
+    const long long rounds = panels * perPanel / slots;
+    if (rounds == 0) return 0;
+    const long long bodyPanels = rounds * slots / perPanel;
+    return bodyPanels >= panels ? M : (int)(bodyPanels * v.BM);
+}
+
+int ridge_gemm_launch_split(int body, int tail, int bodyRows, const void* A, const void* B, void* C, int M, int N,
+                            int K, void* stream) {
+    // Every check before the first launch: a refused call enqueues nothing.
+    if (bodyRows <= 0 || bodyRows >= M) return (int)hipErrorInvalidValue;
+    if (!ridge_gemm_divides(body, bodyRows, N, K) || !ridge_gemm_divides(tail, M - bodyRows, N, K))
+        return (int)hipErrorInvalidValue;
+    if (A == nullptr || B == nullptr || C == nullptr) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 15u) return (int)hipErrorInvalidValue;
+    const char* tailA = static_cast<const char*>(A) + (size_t)bodyRows * K * 2;
+    char* tailC = static_cast<char*>(C) + (size_t)bodyRows * N * 2;
+    const int rc = ridge_gemm_launch(body, A, B, C, bodyRows, N, K, stream);
+    if (rc != 0) return rc;
+    return ridge_gemm_launch(tail, tailA, B, tailC, M - bodyRows, N, K, stream);
 }
 
 size_t ridge_gemm_variant_table_csv(char* buf, size_t cap) {

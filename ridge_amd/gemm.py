@@ -108,6 +108,11 @@ def lib():
     L.ridge_gemm_divides.argtypes = [c_int] * 4
     L.ridge_gemm_launch.restype = c_int
     L.ridge_gemm_launch.argtypes = [c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]
+    L.ridge_gemm_split_rows.restype = c_int
+    L.ridge_gemm_split_rows.argtypes = [c_int] * 5
+    L.ridge_gemm_launch_split.restype = c_int
+    L.ridge_gemm_launch_split.argtypes = [c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                          c_void_p]
     L.ridge_gemm_variant_table_csv.restype = c_size_t
     L.ridge_gemm_variant_table_csv.argtypes = [ctypes.c_char_p, c_size_t]
     L.ridge_fill_uniform_f16.restype = c_int
@@ -200,6 +205,36 @@ def bound_launch(i, A, B, C, M, N, K, stream=None):
         rc = f(*args)
         if rc != HIP_SUCCESS:
             raise RidgeGemmError("ridge_gemm_launch(variant %d, %dx%dx%d) returned hipError %d" % (i, M, N, K, rc))
+    return call
+
+
+def split_rows(body, M, N, K, num_cus=256):
+    """Rows of C a row split gives the body row: whole rounds of its resident
+    workgroups on num_cus CUs (M when the grid already is whole rounds, 0 when it
+    is less than one, -1 for a bad index or a shape the row does not divide)."""
+    return lib().ridge_gemm_split_rows(body, M, N, K, num_cus)
+
+
+def launch_split(body, tail, body_rows, A, B, C, M, N, K, stream=None):
+    """Enqueues C = A B as two launches: variant `body` on rows [0, body_rows),
+    variant `tail` on the rest. Returns the hipError_t value; a refused call
+    enqueues nothing."""
+    return lib().ridge_gemm_launch_split(body, tail, body_rows, _ptr(A), _ptr(B), _ptr(C), M, N, K,
+                                         _stream_handle(stream))
+
+
+def bound_launch_split(body, tail, body_rows, A, B, C, M, N, K, stream=None):
+    """launch_split with its arguments converted once (see bound_launch)."""
+    f = lib().ridge_gemm_launch_split
+    args = (body, tail, body_rows, _ptr(A), _ptr(B), _ptr(C), M, N, K, _stream_handle(stream))
+    keep = (A, B, C, stream)
+
+    def call():
+        assert keep is not None
+        rc = f(*args)
+        if rc != HIP_SUCCESS:
+            raise RidgeGemmError("ridge_gemm_launch_split(%d, %d, %d rows, %dx%dx%d) returned hipError %d"
+                                 % (body, tail, body_rows, M, N, K, rc))
     return call
 
 

@@ -187,3 +187,28 @@ def test_bound_callables_hold_their_operands_and_refuse_a_closed_handle():
         closed.bound_gemm(Operand(), Operand(), Operand(), 256, 256, 64, stream=0)
     with pytest.raises(G.RidgeGemmError, match="closed"):
         closed.gemm(Operand(), Operand(), Operand(), 256, 256, 64, stream=0)
+
+
+def test_row_split_plans_whole_rounds_and_refuses_before_any_launch():
+    """The body row 256x256x32 s3 holds one workgroup per CU (96 KiB of LDS), so on
+    256 CUs a split gives it the rows of whole rounds of 256 tiles, in whole row
+    panels: 6144 x 3072 (24 x 12 = 288 tiles) -> 21 panels = 5376 rows (252 tiles);
+    12288 x 1536 (48 x 6) -> 42 panels; 12288 x 3072 (576 tiles) -> 504 tiles, 42
+    panels. A grid of whole rounds keeps all its rows (M), one below a round none;
+    on 192 CUs 4096^3 (16 x 16 tiles) gets 12 panels. Every refusal comes back
+    before a launch (fake, aligned pointers; no GPU is touched)."""
+    body = G.find_variant(256, 256, 32, 128, 64, 3, 4)
+    tail = G.find_variant(128, 128, 64, 64, 64, 4, 8)
+    assert G.split_rows(body, 6144, 3072, 6144) == 5376
+    assert G.split_rows(body, 12288, 1536, 6144) == 10752
+    assert G.split_rows(body, 12288, 3072, 3072) == 10752
+    assert G.split_rows(body, 4096, 4096, 4096) == 4096
+    assert G.split_rows(body, 4096, 4096, 4096, num_cus=192) == 3072
+    assert G.split_rows(body, 3072, 1536, 3072) == 0
+    assert G.split_rows(body, 6000, 3072, 6144) == -1 and G.split_rows(-1, 6144, 3072, 6144) == -1
+    assert G.split_rows(body, 6144, 3072, 6144, num_cus=0) == -1
+    ok = (16, 32, 48)
+    cases = [(body, tail, 0, ok), (body, tail, 6144, ok), (body, tail, 5300, ok), (body, tail, 5376, (16, 32, 50)),
+             (body, tail, 5376, (0, 32, 48)), (body, -1, 5376, ok), (-1, tail, 5376, ok)]
+    for b, t, rows, ptrs in cases:
+        assert G.launch_split(b, t, rows, *ptrs, 6144, 3072, 6144, 0) == 1, (b, t, rows, ptrs)
