@@ -2,7 +2,8 @@
 """Headline benchmark: FP16 GEMM TFLOP/s at 4096^3 on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--repeats R] [--variant BM,BN,BK,WM,WN,S,G]
-                    [--shape M,N,K] [--no-cpu-baseline] [--no-blaslt] [--no-cold]
+                    [--shape M,N,K] [--split-tail BM,BN,BK,WM,WN,S,G [--split-rows R]]
+                    [--no-cpu-baseline] [--no-blaslt] [--no-cold] [--no-autotune]
                     [--allow-partitioned]
     python bench.py --mode copy     # plain device copy of known size, for scaling
                                     # rocprofv3 FETCH_SIZE / WRITE_SIZE counters
@@ -35,6 +36,14 @@ run on, at most 16).
 
 model: the calibrated cost model's prediction for the measured variant and shape
 (TFLOP/s, label, error against `value`), read from data/hardware/mi355x.json.
+
+--split-tail: a step is a row split instead, two launches on one stream: --variant
+on the first R rows of C (by default the rows of whole rounds of its resident
+workgroups on this device's CUs, ridge_gemm_split_rows) and the tail row on the
+remaining M - R. For grids whose last round of tiles would leave most CUs idle
+(288 tiles of 256x256 on 256 CUs). `config.split` names both halves; the model
+figure is the sum of the two predicted launch times; `roofline.traffic` is null
+(no profile covers a pair of launches).
 
 autotune: the metric's second half, the mean top-10 regret of the model-pruned
 autotuner, is computed from the committed measured sweep (data/measured/mi355x.csv,
@@ -316,6 +325,27 @@ def model_prediction(v, M, N, K, measured):
             "hardware": os.path.relpath(HARDWARE_JSON, ROOT)}
 
 
+def model_split_prediction(body, tail, rows, M, N, K, measured):
+    """The cost model's figure for a row split: the predicted times of the body
+    launch (rows x N x K) and the tail launch ((M - rows) x N x K), added, since
+    the two run one after the other on one stream."""
+    try:
+        from ridge_amd import model as RM
+        hw = RM.Hardware(HARDWARE_JSON)
+        secs, labels = 0.0, []
+        for v, m in ((body, rows), (tail, M - rows)):
+            p = RM.predict(hw, M=m, N=N, K=K, BM=v.BM, BN=v.BN, BK=v.BK, warpM=v.WM, warpN=v.WN,
+                           stages=v.stages, regsPerThread=v.regsPerThread, groupM=v.groupM, schedule=v.schedule)
+            secs += 2.0 * m * N * K / (p["predictedTFLOPS"] * 1e12)
+            labels.append(p["bottleneck"])
+    except Exception as e:  # the model library is part of the build; report its absence
+        return {"error": "%s" % e}
+    tflops = 2.0 * M * N * K / secs / 1e12
+    return {"predicted_tflops": round(tflops, 1), "label": "+".join(labels),
+            "error_pct": round((tflops - measured) / measured * 100, 1),
+            "hardware": os.path.relpath(HARDWARE_JSON, ROOT)}
+
+
 def cpu_baseline(M, N, K, seconds=10.0):
     """f64 oracle GEMM on a block of output rows of the same workload."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -391,6 +421,12 @@ def main():
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--allow-partitioned", action="store_true")
     ap.add_argument("--mode", default="gemm", choices=["gemm", "copy"])
+    ap.add_argument("--split-tail", default=None,
+                    help="tail row BM,BN,BK,WM,WN,S,G of a row split; --variant runs the body rows")
+    ap.add_argument("--split-rows", type=int, default=None,
+                    help="body rows of the split (default: whole rounds of --variant's workgroups)")
+    ap.add_argument("--no-autotune", action="store_true",
+                    help="leave out the autotune regret object (a property of the committed sweeps)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -414,7 +450,26 @@ def main():
     if idx < 0:
         raise SystemExit("variant %s is not in the registered table" % (key,))
     v = G.variant(idx)
-    if not v.divides(M, N, K):
+    split = None
+    if args.split_tail is not None:
+        tidx = G.find_variant(*parse_ints(args.split_tail, 7))
+        if tidx < 0:
+            raise SystemExit("split tail %s is not in the registered table" % (args.split_tail,))
+        rows = args.split_rows
+        if rows is None:
+            rows = G.split_rows(idx, M, N, K, device["cus"])
+            if rows <= 0 or rows >= M:
+                why = ("the row does not divide the shape" if rows < 0 else
+                       "the grid is under one round of resident workgroups" if rows == 0 else
+                       "the grid is a whole number of rounds")
+                raise SystemExit("no row split of %dx%dx%d for %s on %d CUs: %s"
+                                 % (M, N, K, v.label(), device["cus"], why))
+        tv = G.variant(tidx)
+        if not (0 < rows < M and v.divides(rows, N, K) and tv.divides(M - rows, N, K)):
+            raise SystemExit("split of %dx%dx%d at %d rows: %s must divide the body and %s the tail"
+                             % (M, N, K, rows, v.label(), tv.label()))
+        split = (tidx, tv, rows)
+    elif not v.divides(M, N, K):
         raise SystemExit("variant %s does not divide %dx%dx%d" % (v.label(), M, N, K))
 
     dev = torch.device("cuda:0")
@@ -433,7 +488,12 @@ def main():
     # Both kernels are called through one foreign call with pre-converted
     # arguments, so neither side's host cost reaches a window (at 1024^3 a launch
     # is 6 us, about what converting the tensor arguments costs in Python).
-    step = G.bound_launch(idx, A, B, C, M, N, K, stream)
+    def make_step(a, b, c):
+        if split is None:
+            return G.bound_launch(idx, a, b, c, M, N, K, stream)
+        return G.bound_launch_split(idx, split[0], split[2], a, b, c, M, N, K, stream)
+
+    step = make_step(A, B, C)
 
     # Clock ramp: seconds of the same work before anything is timed (the
     # reference warms 5 s, check-gemm.cu:41-45).
@@ -494,10 +554,6 @@ def main():
             fill(Ai, Bi)
             sets.append((Ai, Bi, torch.empty_like(C)))
         torch.cuda.synchronize()
-
-        def make_step(a, b, c):
-            return G.bound_launch(idx, a, b, c, M, N, K, stream)
-
         cold_steps = max(args.steps // 4, 4 * n_sets, COMPARE_LAUNCHES // 2)
         cold_warm_s = max(0.0, min(args.cold_warm_seconds, args.warm_seconds))
         cold_windows = time_cold(make_step, sets, cold_steps, stream, repeats, cold_warm_s)
@@ -506,7 +562,8 @@ def main():
                 "spread": window_summary(flops, cold_windows),
                 "sets": n_sets, "set_bytes": set_bytes, "launches_per_window": cold_steps,
                 "rotation_warm_seconds": cold_warm_s,
-                "roofline": roofline(M, N, K, cold_ms, measured_traffic(M, N, K, key, cold=True))}
+                "roofline": roofline(M, N, K, cold_ms,
+                                     None if split else measured_traffic(M, N, K, key, cold=True))}
         if blas is not None:
             try:
                 blas = G.BlasLt()
@@ -525,7 +582,7 @@ def main():
             cold["frac_of_hipblaslt"] = round(blas_cold_ms / cold_ms, 4)
         del sets
 
-    traffic = measured_traffic(M, N, K, key)
+    traffic = None if split else measured_traffic(M, N, K, key)
 
     out = {
         "metric": "FP16 GEMM TFLOP/s @4096^3 on 1 MI355X (% MFMA peak, % hipBLASLt); top-10 regret"
@@ -565,11 +622,18 @@ def main():
                             "ours_tflops": round(ours, 3),
                             "basis": "HIP events, %d windows of %d launches, middle window" % (repeats, compare_steps),
                             "frac_of_hipblaslt": round(ours / best, 4)}
+    if split is not None:
+        out["config"]["split"] = {"body_rows": split[2], "tail": split[1].label(), "tail_rows": M - split[2],
+                                  "body_rows_planned": args.split_rows is None}
     if cold is not None:
         out["cold"] = cold
     out["device"] = device
-    out["autotune"] = autotune_regret(10)
-    out["model"] = model_prediction(v, M, N, K, value)
+    if not args.no_autotune:
+        out["autotune"] = autotune_regret(10)
+    if split is None:
+        out["model"] = model_prediction(v, M, N, K, value)
+    else:
+        out["model"] = model_split_prediction(v, split[1], split[2], M, N, K, value)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)
         out["cpu_baseline_naive_1core"] = cpu_baseline_naive_1core()

@@ -492,6 +492,93 @@ def test_reported_rows_every_output(shape, key):
     assert ok, "FP16-output gate: frob %.3e, worst element at %.2f of its bound" % (frob, worst)
 
 
+# Row split: the 256x256 s3 row on the rows of whole rounds of tiles and another
+# row on the rest (two launches, ridge_gemm_launch_split).
+SPLIT_BODY = (256, 256, 32, 128, 64, 3, 4)
+SPLIT_TAILS = [(128, 128, 64, 64, 64, 4, 8), (256, 128, 64, 64, 64, 3, 8), (64, 64, 64, 32, 32, 4, 8),
+               (128, 64, 128, 64, 32, 3, 8)]
+
+
+def test_row_split_small_integers_bit_exact_and_nothing_outside_c():
+    """6144 x 3072 x 256 on integers in [-3, 3] (exact sums): the split gives the
+    exact product rounded once, bit for bit, with the planner's split (5376 body
+    rows on 256 CUs) for four tails, a 64-row tail and a one-panel body; C is a
+    view of a buffer with 64 guard rows after it, which keep their bits; one case
+    runs on a side stream."""
+    M, N, K = 6144, 3072, 256
+    body = G.find_variant(*SPLIT_BODY)
+    assert body >= 0 and G.split_rows(body, M, N, K, 256) == 5376
+    Ab, Bb, want = _exact_case(M, N, K, -3, 3, 6144 + 3072 + 256)
+    A, B = _to_dev(Ab.ravel(), (M, K)), _to_dev(Bb.ravel(), (K, N))
+    cases = [(G.find_variant(*t), 5376) for t in SPLIT_TAILS]
+    cases += [(G.find_variant(64, 64, 64, 32, 32, 4, 8), M - 256), (G.find_variant(*SPLIT_TAILS[0]), 256)]
+    side = torch.cuda.Stream()
+    for n, (tail, rows) in enumerate(cases):
+        assert tail >= 0
+        on_side = n == 1
+        print("split %s | %s at %d rows%s" % (G.variant(body).label(), G.variant(tail).label(), rows,
+                                              " (side stream)" if on_side else ""), flush=True)
+        buf = torch.full((M + 64, N), float("nan"), dtype=torch.float16, device=DEV)
+        C = buf[:M]
+        if on_side:
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                rc = G.launch_split(body, tail, rows, A, B, C, M, N, K, stream=side)
+            side.synchronize()
+        else:
+            rc = G.launch_split(body, tail, rows, A, B, C, M, N, K)
+            torch.cuda.synchronize()
+        assert rc == 0
+        got = _bits(C)
+        bad = int(np.count_nonzero(got != want))
+        assert bad == 0, "%d of %d outputs differ (first at row %d)" % (
+            bad, M * N, int(np.flatnonzero(got != want)[0]) // N if bad else -1)
+        guard = _bits(buf[M:])
+        assert np.all(guard == guard[0]) and np.isnan(O.f16_bits_to_f32(guard[:1]))[0], "guard rows written"
+
+
+def test_row_split_halves_equal_their_own_launches_and_the_oracle():
+    """12288 x 3072 x 3072 on U[-1,1) inputs with the planner's split for this
+    device: the body rows equal the body row's single launch over the whole shape
+    bit for bit (a tile's sum does not depend on the grid), the tail rows equal
+    the tail row launched alone on A's last rows, and every tail row plus 128
+    body rows pass the FP16-output gate against the f64 oracle. Tails: a
+    one-tile-per-workgroup row and a persistent row (whose K loop starts at a
+    tile-dependent K tile, so it is compared with its own launch)."""
+    M, N, K = 12288, 3072, 3072
+    body = G.find_variant(*SPLIT_BODY)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rows = G.split_rows(body, M, N, K, cus)
+    print("device CUs %d, body rows %d" % (cus, rows), flush=True)
+    if not 0 < rows < M:
+        pytest.skip("no split of %dx%dx%d on %d CUs" % (M, N, K, cus))
+    A = torch.empty((M, K), dtype=torch.float16, device=DEV)
+    B = torch.empty((K, N), dtype=torch.float16, device=DEV)
+    G.fill_uniform(A, 11)
+    G.fill_uniform(B, 12)
+    single = _bits(_run(body, A, B, M, N, K)).reshape(M, N)
+    Ab, Bb = _bits(A), _bits(B)
+    sample = np.concatenate([np.linspace(0, rows - 1, 128).astype(int), np.arange(rows, M)])
+    Abs = Ab.reshape(M, K)[sample].ravel()
+    ref = O.gemm_f64(Abs, Bb, len(sample), N, K)
+    absprod = O.gemm_f64(O.abs_bits(Abs), O.abs_bits(Bb), len(sample), N, K)
+    for key in ((256, 128, 64, 64, 64, 3, 8), (256, 128, 32, 64, 64, 6, 4)):
+        tail = G.find_variant(*key)
+        print("  tail %s, %d rows" % (G.variant(tail).label(), M - rows), flush=True)
+        C = torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV)
+        assert G.launch_split(body, tail, rows, A, B, C, M, N, K) == 0
+        torch.cuda.synchronize()
+        got = _bits(C).reshape(M, N)
+        assert np.array_equal(got[:rows], single[:rows]), "body rows differ from the single launch"
+        alone = _bits(_run(tail, A[rows:], B, M - rows, N, K)).reshape(M - rows, N)
+        assert np.array_equal(got[rows:], alone), "tail rows differ from the tail row's own launch"
+        ok, frob, worst = O.passes_fp16(O.f16_bits_to_f32(got[sample].ravel()).reshape(len(sample), N),
+                                        ref, absprod, K)
+        print("  FP16-output gate on %d rows: frob %.3e, worst element at %.3f of its bound"
+              % (len(sample), frob, worst), flush=True)
+        assert ok, "FP16-output gate: frob %.3e, worst element at %.2f of its bound" % (frob, worst)
+
+
 def test_hipblaslt_comparator_agrees_with_oracle():
     M, N, K = 512, 768, 256
     Ab = O.lcg_fill_f16(M * K, 5)
