@@ -335,8 +335,12 @@ int main(int argc, char** argv) {
             const Timing t = timeTflops([&] { launch(); }, flops);
             if (++tally.measured % kCanaryPeriod == 0) readCanary();
             emit(planRow(p, t, blasTflops, canary.last()));
-            std::printf("    row %2d on %5d rows + row %2d  %8.2f TFLOP/s  %6.3f x hipBLASLt\n", p.body, p.bodyRows,
-                        p.tail, t.tflops, t.tflops / blasTflops);
+            if (p.split())
+                std::printf("    row %2d on %5d rows + row %2d  %8.2f TFLOP/s  %6.3f x hipBLASLt\n", p.body,
+                            p.bodyRows, p.tail, t.tflops, t.tflops / blasTflops);
+            else
+                std::printf("    row %2d alone               %8.2f TFLOP/s  %6.3f x hipBLASLt\n", p.body, t.tflops,
+                            t.tflops / blasTflops);
             std::fflush(stdout);
         }
     }

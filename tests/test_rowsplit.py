@@ -182,3 +182,28 @@ def test_registered_plan_list_regenerates_from_the_committed_inputs(tmp_path):
            for s in shapes]
     assert sorted(per).count(5) == 77 and sorted(per).count(3) == 12
     assert sum(r["role"] == "model_single" for r in committed) == 33
+
+
+def test_registered_row_split_measurement_figures():
+    """The registered measurement (data/sweep/mi355x-rowsplit.md) scored with its
+    frozen constants: a split pays on three shapes; C1 (every split the model picks
+    beats the single row) fails, 3 of 5; C2 (splits among the candidates lower the
+    model's mean regret) passes, 1.40% against 1.73%."""
+    ranker = R.Ranker(os.path.join(ROOT, "data", "sweep", "mi355x-rowsplit-hw.json"))
+    rows = R.score(os.path.join(ROOT, "data", "sweep", "mi355x-rowsplit-plans.csv"),
+                   os.path.join(ROOT, "data", "measured", "mi355x-rowsplit.csv"), ranker)
+    assert len(rows) == 89
+    wins = sorted(((r["M"], r["N"], r["K"]), round(r["gain"], 3)) for r in rows if r["gain"] > 1.05)
+    assert wins == [((6144, 3072, 6144), 1.164), ((12288, 1536, 6144), 1.171), ((12288, 3072, 3072), 1.055)]
+    assert sum(r["gain"] > 1.01 for r in rows) == 3
+    picks = {(r["M"], r["N"], r["K"]): r for r in rows if r["model_picks_split"]}
+    assert sorted(picks) == [(1536, 6144, 2048), (5120, 5120, 3072), (6144, 3072, 6144), (12288, 1536, 6144),
+                             (12288, 3072, 3072)]
+    assert sum(r["regret_with_splits"] == 0.0 for r in picks.values()) == 3
+    assert picks[(5120, 5120, 3072)]["regret_with_splits"] == pytest.approx(13.258, abs=1e-3)
+    assert picks[(1536, 6144, 2048)]["regret_with_splits"] == pytest.approx(8.16, abs=1e-2)
+    mean = lambda xs: sum(xs) / len(xs)
+    assert mean([r["regret_with_splits"] for r in rows]) == pytest.approx(1.398, abs=1e-3)
+    assert mean([r["regret_singles"] for r in rows]) == pytest.approx(1.729, abs=1e-3)
+    assert max(r["regret_singles"] for r in rows) == pytest.approx(20.037, abs=1e-3)
+    assert sum(r["best_vs_blas"] > 1 for r in rows) == 89 and sum(r["best_single_vs_blas"] > 1 for r in rows) == 86

@@ -72,7 +72,7 @@ def test_ridge_measure_times_registered_launch_plans(tmp_path):
                            "--warmup-seconds", "1", "--settle-seconds", "0.05"],
                           cwd=ROOT, capture_output=True, text=True, timeout=300)
     assert proc.returncode == 0, proc.stdout[-4000:] + proc.stderr[-2000:]
-    assert proc.stdout.count("hipBLASLt") == 1
+    assert proc.stdout.count("1536x1536x512  hipBLASLt") == 1
     rows = list(csv.DictReader(l for l in out.read_text().splitlines() if not l.startswith("#")))
     assert [int(r["body_rows"]) for r in rows] == [1536, 1024]
     assert [int(r["schedule"]) for r in rows] == [1, 0] and [int(r["tail_schedule"]) for r in rows] == [-1, 2]
