@@ -46,8 +46,10 @@ figure is the sum of the two predicted launch times; `roofline.traffic` is null
 (no profile covers a pair of launches).
 
 autotune: the metric's second half, the mean top-10 regret of the model-pruned
-autotuner, is computed from the committed measured sweep (data/measured/mi355x.csv,
-14 shapes x 24 variants) and the committed calibration (data/hardware/mi355x.json)
+autotuner, is computed from the committed measured sweep of the current kernels
+(data/measured/mi355x-steady-loop.csv, 14 shapes x 24 variants; the same sweep with
+the previous kernels, data/measured/mi355x.csv, beside it) and the committed
+calibration (data/hardware/mi355x.json)
 by ridge_amd.autotune, with regret at top-1 and the expected regret of a random
 shortlist beside it, and the same for the seven held-out sweeps, each registered
 before it was measured and scored with the constants frozen beside it
@@ -72,7 +74,11 @@ DEFAULT_SHAPE = (4096, 4096, 4096)
 # measurement, data/measured/mi355x-baseline-configs.csv).
 DEFAULT_VARIANT = (256, 256, 32, 128, 64, 3, 4)
 PROFILES = os.path.join(ROOT, "profiles")
-MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x.csv")
+# The in-sample sweep measured with the current kernels, and the same sweep with
+# the kernels before the steady K-loop passes (the set every earlier figure and
+# the held-out comparisons refer to).
+MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-steady-loop.csv")
+MEASURED_SWEEP_PREVIOUS = os.path.join(ROOT, "data", "measured", "mi355x.csv")
 HARDWARE_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
 HELDOUT_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout.csv")
 HELDOUT_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout-hw.json")
@@ -272,16 +278,19 @@ def measured_traffic(M, N, K, key, cold=False):
 
 def autotune_regret(k=10):
     """The pruner's regret at top-1 and top-k with the random-shortlist baseline,
-    on the committed in-sample sweep (data/measured/mi355x.csv, 14 shapes x 24
-    variants, current calibration) and on the seven held-out sweeps, each
+    on the committed in-sample sweep measured with the current kernels
+    (data/measured/mi355x-steady-loop.csv, 14 shapes x 24 variants, current
+    calibration), on the same sweep with the previous kernels
+    (data/measured/mi355x.csv) and on the seven held-out sweeps, each
     registered before it was measured and scored with the constants frozen with
     it (data/measured/mi355x-heldout*.csv); a property of the
     sweeps and the model, not of this run's timing. None of it is computed if
     the model CLI is not built."""
     try:
         from ridge_amd import autotune as AT
-        out = {"top_k": k, "source": "data/measured/mi355x.csv"}
+        out = {"top_k": k, "source": os.path.relpath(MEASURED_SWEEP, ROOT)}
         for name, measured, hw in (("in_sample", MEASURED_SWEEP, HARDWARE_JSON),
+                                   ("in_sample_previous_kernels", MEASURED_SWEEP_PREVIOUS, HARDWARE_JSON),
                                    ("held_out", HELDOUT_SWEEP, HELDOUT_HARDWARE_JSON),
                                    ("held_out_2", HELDOUT2_SWEEP, HELDOUT2_HARDWARE_JSON),
                                    ("held_out_3", HELDOUT3_SWEEP, HELDOUT3_HARDWARE_JSON),
