@@ -508,3 +508,27 @@ def test_seventh_heldout_figures_as_reported():
     assert by_k[10]["mean_regret"] == 0.0 and by_k[10]["hits"] == 14
     base = AT.baselines(MEASURED7, FROZEN7, ks=(1, 10))
     assert base[1]["random"][0] == pytest.approx(19.07, abs=0.01)
+
+
+# The eighth held-out sweep (data/sweep/mi355x-heldout8.md).
+REGISTERED8 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout8-registered.csv")
+FROZEN8 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout8-hw.json")
+TABLE8 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout8-table.csv")
+
+
+def test_eighth_heldout_registration():
+    """14 shapes from value sets no earlier set could hold, none in an earlier set;
+    the seventh set's table; the seventh set's constants unchanged."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED8)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, REGISTERED6,
+                 REGISTERED7, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    values = (2560, 3584, 7168, 10240, 14336)
+    assert len(held) == 14 and not held & earlier
+    assert all(M in values and N in values and K in (384, 1536, 2560, 5120) for M, N, K in held)
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE8) == keys(TABLE7) == list(V.kernel_table_keys())
+    assert json.load(open(FROZEN8)) == json.load(open(FROZEN7))
