@@ -130,6 +130,15 @@ struct HardwareModel {
                                      //    once and the L2s' further misses (other XCDs re-fetching the
                                      //    same panels) are MALL hits at mallRefillBytesPerSec, in series
     double mallBytes = 0.0;          // capacity of the memory-side cache in front of HBM (datasheet)
+    int mallWriteModel = 0;          // 0: C drains at hbmWriteBytesPerSec, shared by every CU
+                                     //    (hbmWriteModel 1)
+                                     // 1: the last drain's cached stores of C (every schedule but the
+                                     //    persistent one, whose stores are non-temporal) go to the MALL
+                                     //    when A, B and C together fit in it (mallBytes), at
+                                     //    mallWriteBytesPerSec, shared by the CUs that hold a
+                                     //    workgroup, not by all; a drain to HBM and the DRAM-side write
+                                     //    time are unchanged
+    double mallWriteBytesPerSec = 0.0;  // [CAL] 16-byte cached stores into a MALL-resident buffer (cal-hbm-bw)
     int fillShareModel = 0;          // 0: every workgroup fetches its first tiles from HBM (reference)
                                      // 1: the resident workgroups' first tiles come from HBM once per
                                      //    distinct panel an XCD holds (the kernels' launch order) and

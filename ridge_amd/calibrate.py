@@ -110,6 +110,10 @@ def band_check(res, spec):
     if "fillLatencySec" in res:
         ok &= check("fillLatencySec", res["fillLatencySec"] * 1e6, 0.2, 10.0, "us",
                     "first-tile wait of a whole grid from HBM")
+    if "mallWriteBytesPerSec" in res and "hbmWriteBytesPerSec" in res:
+        ok &= check("mallWriteBytesPerSec", res["mallWriteBytesPerSec"] / 1e12, 0.9 * res["hbmWriteBytesPerSec"] / 1e12,
+                    4.0 * spec["hbm_bytes_per_sec"] / 1e12, "TB/s",
+                    "cached stores into a MALL-resident buffer: not slower than to HBM")
     for i in (1, 2):
         key = "persistentStepCycles%d" % i
         if key in res and "pingPongMfmaCycles" in res:
@@ -232,7 +236,7 @@ def hardware_json(res, spec, arch):
     # that reads them switched on) when the log has them.
     for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec", "persistentStepCycles1",
                  "persistentStepCycles2", "persistentTileCycles1", "persistentTileCycles2", "launchSeconds",
-                 "launchOverheadSeconds", "launchIsolatedSeconds"] +
+                 "launchOverheadSeconds", "launchIsolatedSeconds", "mallWriteBytesPerSec"] +
                 ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
         if key in res:
             out[key] = res[key]
@@ -249,6 +253,7 @@ def hardware_json(res, spec, arch):
                         ("mallStreamModel", ["mallRefillBytesPerSec"] + ["mallStretch%d" % i for i in range(5)]),
                         ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"]),
                         ("launchModel", ["launchOverheadSeconds"]),
+                        ("mallWriteModel", ["mallWriteBytesPerSec", "hbmWriteBytesPerSec", "mallRefillBytesPerSec"]),
                         ("labelModel", ["launchIsolatedSeconds", "hbmWriteBytesPerSec"])):
         if all(k in res for k in needs):
             out[term] = 1

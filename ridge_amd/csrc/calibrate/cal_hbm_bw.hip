@@ -19,11 +19,18 @@
 // writes its C this way). fillLatencySec is the wait of a workgroup's first
 // load when a whole grid starts at once and the data comes from HBM. A 64 MiB buffer (MALL-resident) is also timed and reported as information:
 // that is the level that serves cross-XCD panel re-reads in the GEMM.
+// mallWriteBytesPerSec is the rate of cached 16-byte stores into a 64 MiB buffer,
+// which the 256 MiB MALL holds: 16 GiB of stores wrapped into it, swept like the
+// streams above. It is the rate a GEMM's C drains at when A, B and C stay in the
+// MALL, as they do when the same operands are timed launch after launch.
+// `cal-hbm-bw --mall-write-only` measures that constant alone.
 // l2HitBytesPerCycle times the same kind of read (16 GiB of it) with every index
 // wrapped into a 1 MiB buffer, which each XCD's L2 holds, in shader cycles: the
 // rate at which the L2s serve tiles that every workgroup re-reads (the shared
 // operand of a skinny GEMM).
 #include "cal_common.hpp"
+
+#include <string>
 
 using namespace ridgecal;
 
@@ -85,6 +92,22 @@ __global__ __launch_bounds__(kLanes) void streamWriteKernel(float4_t* __restrict
         }
         v[2] += 1.0f;
         p += Flight * stride;
+    }
+}
+
+// The write stream with every chunk index wrapped into the first `mask + 1` (a
+// power of two) chunks of the buffer: `passes` passes of Flight stores per lane
+// move far more bytes than the buffer holds, so one launch lasts milliseconds.
+template <int Flight>
+__global__ __launch_bounds__(kLanes) void wrappedWriteKernel(float4_t* __restrict__ dst, size_t passes, size_t mask) {
+    const size_t stride = size_t(gridDim.x) * kLanes;
+    size_t i = size_t(blockIdx.x) * kLanes + threadIdx.x;
+    float4_t v = {float(threadIdx.x), float(blockIdx.x), 0.5f, -0.25f};
+    for (size_t pass = 0; pass < passes; ++pass) {
+#pragma unroll
+        for (int j = 0; j < Flight; ++j) dst[(i + j * stride) & mask] = v;
+        v[2] += 1.0f;
+        i += Flight * stride;
     }
 }
 
@@ -263,9 +286,73 @@ void sweepWrites(std::vector<ReadPoint>& out, float4_t* dst, size_t bytes, int c
     out.push_back(timeRead<4, NonTemporal, true>(dst, bytes, nullptr, cus, wgPerCu));
 }
 
+// Middle over kRepeats of the wrapped write stream: `totalBytes` of cached stores
+// into the first `wrapBytes` (a power of two) of `buf`.
+template <int Flight>
+ReadPoint timeWrappedWrite(float4_t* buf, size_t wrapBytes, size_t totalBytes, int cus, int wgPerCu) {
+    ReadPoint pt;
+    pt.flight = Flight;
+    pt.wgPerCu = wgPerCu;
+    const int blocks = cus * wgPerCu;
+    const size_t chunksPerPass = size_t(blocks) * kLanes * Flight;
+    const size_t passes = totalBytes / sizeof(float4_t) / chunksPerPass;
+    const size_t mask = wrapBytes / sizeof(float4_t) - 1;
+    const double bytes = double(passes * chunksPerPass * sizeof(float4_t));
+    hipEvent_t e0, e1;
+    CAL_HIP_CHECK(hipEventCreate(&e0));
+    CAL_HIP_CHECK(hipEventCreate(&e1));
+    for (int r = 0; r < kRepeats; ++r) {
+        hipLaunchKernelGGL((wrappedWriteKernel<Flight>), dim3(blocks), dim3(kLanes), 0, nullptr, buf, passes, mask);
+        CAL_HIP_CHECK(hipDeviceSynchronize());
+        CAL_HIP_CHECK(hipEventRecord(e0, nullptr));
+        hipLaunchKernelGGL((wrappedWriteKernel<Flight>), dim3(blocks), dim3(kLanes), 0, nullptr, buf, passes, mask);
+        CAL_HIP_CHECK(hipEventRecord(e1, nullptr));
+        CAL_HIP_CHECK(hipEventSynchronize(e1));
+        CAL_HIP_CHECK(hipGetLastError());
+        float ms = 0.0f;
+        CAL_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        pt.reps.push_back(bytes / (double(ms) * 1e-3));
+    }
+    CAL_HIP_CHECK(hipEventDestroy(e0));
+    CAL_HIP_CHECK(hipEventDestroy(e1));
+    pt.bytesPerSec = middle(pt.reps);
+    return pt;
+}
+
+// The MALL write sweep: 16 GiB of cached stores wrapped into the first 64 MiB of
+// `buf`. Prints the curve; returns false when no point had stable repeats.
+bool mallWrite(float4_t* buf, int cus, double& rate) {
+    constexpr size_t kWrap = 64ull << 20;
+    constexpr size_t kTotal = 16ull << 30;
+    std::printf("\nMALL-resident cached stores, 16 GiB wrapped into %.0f MiB, 256-lane workgroups, 16-byte stores\n",
+                kWrap / double(1ull << 20));
+    std::printf("  %8s %10s %6s %12s %10s\n", "per pass", "WG per CU", "nt", "GB/s", "range");
+    std::vector<ReadPoint> curve;
+    for (int wgPerCu : {2, 4, 8}) {
+        curve.push_back(timeWrappedWrite<1>(buf, kWrap, kTotal, cus, wgPerCu));
+        curve.push_back(timeWrappedWrite<2>(buf, kWrap, kTotal, cus, wgPerCu));
+        curve.push_back(timeWrappedWrite<4>(buf, kWrap, kTotal, cus, wgPerCu));
+    }
+    printCurve("mallWrite", curve);
+    const ReadPoint* best = stableMaximum(curve);
+    if (!best) {
+        std::fprintf(stderr, "no configuration of the MALL write had stable repeats\n");
+        return false;
+    }
+    rate = best->bytesPerSec;
+    std::printf("\nlargest stable point: %d stores per lane per pass, %d workgroups per CU\n", best->flight,
+                best->wgPerCu);
+    return reportConstant("mallWriteBytesPerSec", rate / 1e9, "GB/s", best->reps);
+}
+
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
+    const bool mallWriteOnly = argc > 1 && std::string(argv[1]) == "--mall-write-only";
+    if (argc > 1 && !mallWriteOnly) {
+        std::fprintf(stderr, "usage: cal-hbm-bw [--mall-write-only]\n");
+        return 2;
+    }
     const hipDeviceProp_t prop = deviceBanner();
     constexpr size_t kBytes = 4ull << 30;
     constexpr size_t kMallBytes = 64ull << 20;
@@ -283,6 +370,14 @@ int main() {
     CAL_HIP_CHECK(hipMemset(src, 1, kBytes));
     warmUp();
     const int cus = prop.multiProcessorCount;
+    if (mallWriteOnly) {
+        double mallWriteRate = 0.0;
+        const bool ok = mallWrite(src, cus, mallWriteRate);
+        if (ok) std::printf("\nCAL_RESULT mallWriteBytesPerSec %.6e\n", mallWriteRate);
+        CAL_HIP_CHECK(hipFree(src));
+        CAL_HIP_CHECK(hipFree(sink));
+        return ok ? 0 : 1;
+    }
     std::printf("\nHBM streaming read, %.2f GiB buffer, 256-lane workgroups, 16-byte loads\n",
                 kBytes / double(1ull << 30));
     std::printf("  %8s %10s %6s %12s %10s\n", "in flight", "WG per CU", "nt", "GB/s", "range");
@@ -367,12 +462,15 @@ int main() {
     std::printf("  (16 GiB of reads wrapped into 1 MiB, served by the XCDs' L2s: %.1f TB/s at %.0f MHz)\n",
                 l2 * l2Clock / 1e12, l2Clock / 1e6);
     CAL_HIP_CHECK(hipFree(dStamps));
+    double mallWriteRate = 0.0;
+    const bool mallWriteStable = mallWrite(src, cus, mallWriteRate);
     std::printf("\nCAL_RESULT hbmBytesPerSec %.6e\n", hbm);
     std::printf("CAL_RESULT hbmWriteBytesPerSec %.6e\n", hbmWrite);
     std::printf("CAL_RESULT fillLatencySec %.6e\n", fillLatency);
     std::printf("CAL_RESULT mallBytesPerSec %.6e\n", mall);
     std::printf("CAL_RESULT l2HitBytesPerCycle %.6f\n", l2);
+    if (mallWriteStable) std::printf("CAL_RESULT mallWriteBytesPerSec %.6e\n", mallWriteRate);
     CAL_HIP_CHECK(hipFree(src));
     CAL_HIP_CHECK(hipFree(sink));
-    return stable && writeStable && latStable && l2Stable ? 0 : 1;
+    return stable && writeStable && latStable && l2Stable && mallWriteStable ? 0 : 1;
 }

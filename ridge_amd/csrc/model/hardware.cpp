@@ -124,6 +124,7 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         I("persistentTileModel", h.persistentTileModel), R("persistentTileCycles1", h.persistentTileCycles[0]),
         R("persistentTileCycles2", h.persistentTileCycles[1]),
         I("fillShareModel", h.fillShareModel), I("mallReuseModel", h.mallReuseModel), R("mallBytes", h.mallBytes),
+        I("mallWriteModel", h.mallWriteModel), R("mallWriteBytesPerSec", h.mallWriteBytesPerSec),
         I("launchModel", h.launchModel), R("launchOverheadSeconds", h.launchOverheadSeconds),
         R("launchIsolatedSeconds", h.launchIsolatedSeconds), I("labelModel", h.labelModel),
         R("nominalClockHz", h.nominalClockHz),
@@ -179,7 +180,8 @@ std::string inconsistency(const HardwareModel& h) {
         {"fillLatencyModel", h.fillLatencyModel, 1}, {"mallStreamModel", h.mallStreamModel, 1},
         {"persistentStepModel", h.persistentStepModel, 1}, {"persistentTileModel", h.persistentTileModel, 1},
         {"fillShareModel", h.fillShareModel, 1},
-        {"mallReuseModel", h.mallReuseModel, 1}, {"launchModel", h.launchModel, 1},
+        {"mallReuseModel", h.mallReuseModel, 1}, {"mallWriteModel", h.mallWriteModel, 1},
+        {"launchModel", h.launchModel, 1},
         {"labelModel", h.labelModel, 2},
     };
     for (const auto& s : switches)
@@ -216,6 +218,9 @@ std::string inconsistency(const HardwareModel& h) {
         return "fillShareModel 1 reads l2HitBytesPerCycle, which must be positive";
     if (h.mallReuseModel == 1 && !(h.mallRefillBytesPerSec > 0.0 && h.mallBytes > 0.0))
         return "mallReuseModel 1 reads mallRefillBytesPerSec and mallBytes, which must be positive";
+    if (h.mallWriteModel == 1 && !(h.hbmWriteModel == 1 && h.mallWriteBytesPerSec > 0.0 && h.mallBytes > 0.0))
+        return "mallWriteModel 1 refines hbmWriteModel 1 and reads mallWriteBytesPerSec and mallBytes, which must be "
+               "positive";
     if (h.persistentStepModel == 1 && !(h.persistentStepCycles[0] > 0.0 && h.persistentStepCycles[1] > 0.0))
         return "persistentStepModel 1 reads persistentStepCycles1 and persistentStepCycles2, which must be positive";
     if (h.persistentTileModel == 1 && !(h.persistentTileCycles[0] >= 0.0 && h.persistentTileCycles[1] >= 0.0 &&

@@ -67,6 +67,10 @@
 //   write overlap         = hw.writeOverlapModel 1: C's writes to DRAM overlap
 //                           the tile loads the L2s serve; the DRAM reads come
 //                           before both (reference: one DRAM stream)
+//   MALL drain            = hw.mallWriteModel 1: the last drain of cached C
+//                           stores goes to the MALL when A, B and C fit it, at
+//                           the MALL's write rate shared by the CUs holding a
+//                           workgroup (reference: the DRAM rate over all SMs)
 //   persistent tiles      = hw.persistentTileModel 1: every tile a persistent
 //                           workgroup walks adds the epilogue its compute waves
 //                           run before the next one, as the same skeleton with
@@ -417,8 +421,23 @@ Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
         tPrologue *= std::min(1.0, shared / (allBytes / hw.hbmBytesPerSec));
     }
     // hbmWriteModel 1: the drain moves at the streaming-write rate.
+    // mallWriteModel 1: the last drain's cached stores of C (all but the
+    // persistent rows, which store non-temporally) land in the MALL when A, B and
+    // C fit in it, at the MALL's write rate, shared by the CUs that hold a
+    // workgroup (a grid of fewer workgroups than CUs leaves some idle). A drain to
+    // HBM keeps the streaming-write rate over all CUs. The DRAM-side write time
+    // below keeps the streaming-write rate too: a write-bound row's sustained C
+    // stream does not reach the MALL's rate (measured 2.6-3.3 TB/s at 8192 x 2048
+    // x 128 with C in the MALL).
+    const bool cachedC = hw.mallWriteModel == 1 && !persistent &&
+                         (double(cfg.M) * cfg.K + double(cfg.K) * cfg.N) * db +
+                                 double(cfg.M) * cfg.N * hw.cBytes <= hw.mallBytes;
+    const double writeRate = cachedC ? hw.mallWriteBytesPerSec : hw.hbmWriteBytesPerSec;
+    // The dispatcher gives each workgroup a CU of its own while CUs are free.
+    const double drainers =
+        cachedC ? std::max(1.0, std::min(double(hw.numSMs), std::min(totalCtas, ctaSlots))) : double(hw.numSMs);
     const double drainBytesPerCycle =
-        hw.hbmWriteModel == 1 ? hw.hbmWriteBytesPerSec / (hw.clockHz * double(hw.numSMs)) : gmemBytesPerCycle;
+        hw.hbmWriteModel == 1 ? writeRate / (hw.clockHz * drainers) : gmemBytesPerCycle;
     const double tEpilogue = double(cfg.BM) * cfg.BN * double(hw.cBytes) / drainBytesPerCycle / ctasPerSM;
     const double tBody = kSteps * tStep;
     double envelopeEfficiency;

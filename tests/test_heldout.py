@@ -339,49 +339,57 @@ def test_sixth_heldout_figures_as_reported():
 CURRENT_HW = os.path.join(ROOT, "data", "hardware", "mi355x.json")
 
 
-# (MAPE, regret at k = 1 mean and worst) per committed measurement, with the
-# current model and with its writeOverlapModel switched off (the model before it).
+# (MAPE, regret at k = 1 mean and worst, regret at k = 10) per committed
+# measurement: with the current model, with its mallWriteModel switched off (the
+# model every held-out set up to the eighth was scored against), and with its
+# writeOverlapModel switched off.
 CURRENT_FIGURES = [
-    ("mi355x.csv", (8.93, 1.19, 6.57), (9.89, 1.19, 6.57)),
-    ("mi355x-replicate.csv", (8.41, 1.02, 8.86), (8.97, 1.02, 8.86)),
-    ("mi355x-baseline-configs.csv", (12.68, 9.91, 27.95), (14.38, 9.91, 27.95)),
-    ("mi355x-heldout.csv", (7.64, 1.38, 11.04), (7.60, 1.41, 11.04)),
-    ("mi355x-heldout2.csv", (11.33, 2.00, 8.22), (11.26, 2.20, 8.22)),
-    ("mi355x-heldout3.csv", (8.41, 0.50, 4.19), (10.00, 0.50, 4.15)),
-    ("mi355x-heldout4.csv", (10.10, 1.87, 13.04), (10.11, 1.98, 13.04)),
-    ("mi355x-heldout5.csv", (8.04, 1.88, 12.23), (8.10, 1.88, 12.23)),
-    ("mi355x-heldout6.csv", (8.18, 2.01, 15.43), (8.78, 2.04, 15.43)),
-    ("mi355x-heldout7.csv", (9.26, 2.08, 10.16), (8.76, 2.93, 11.03)),
+    ("mi355x.csv", (7.69, 1.19, 6.57, 0.0), (8.93, 1.19, 6.57, 0.0), (8.72, 3.24, 12.63, 0.30)),
+    ("mi355x-replicate.csv", (8.08, 1.02, 8.86, 0.0), (8.41, 1.02, 8.86, 0.0), (8.65, 4.20, 18.54, 0.07)),
+    ("mi355x-baseline-configs.csv", (11.46, 9.91, 27.95, 0.0), (12.68, 9.91, 27.95, 0.0),
+     (13.50, 14.32, 27.95, 0.0)),
+    ("mi355x-heldout.csv", (8.81, 1.41, 11.04, 0.0), (7.64, 1.38, 11.04, 0.0), (8.73, 1.42, 11.04, 0.55)),
+    ("mi355x-heldout2.csv", (11.61, 2.20, 8.22, 0.0), (11.33, 2.00, 8.22, 0.0), (11.37, 3.36, 10.50, 0.0)),
+    ("mi355x-heldout3.csv", (8.11, 0.50, 4.19, 0.0), (8.41, 0.50, 4.19, 0.0), (9.84, 4.16, 23.38, 0.06)),
+    ("mi355x-heldout4.csv", (11.48, 1.98, 13.04, 0.0), (10.10, 1.87, 13.04, 0.0), (11.36, 1.98, 13.04, 0.0)),
+    ("mi355x-heldout5.csv", (8.28, 1.88, 12.23, 0.0), (8.04, 1.88, 12.23, 0.0), (8.30, 2.38, 12.23, 0.0)),
+    ("mi355x-heldout6.csv", (8.74, 2.01, 15.43, 0.0), (8.18, 2.01, 15.43, 0.0), (9.34, 2.15, 15.43, 0.12)),
+    ("mi355x-heldout7.csv", (8.65, 2.08, 10.16, 0.0), (9.26, 2.08, 10.16, 0.0), (8.17, 2.55, 10.16, 0.0)),
     # The in-sample shapes re-measured with the steady-pass kernels.
-    ("mi355x-steady-loop.csv", (9.07, 0.70, 5.92), (9.80, 0.70, 5.92)),
-    ("mi355x-heldout8.csv", (8.91, 2.69, 19.66), (8.43, 1.12, 9.51)),
+    ("mi355x-steady-loop.csv", (7.30, 0.70, 5.92, 0.0), (9.07, 0.70, 5.92, 0.0), (7.99, 3.39, 15.05, 0.05)),
+    ("mi355x-heldout8.csv", (7.20, 1.23, 5.85, 0.0), (8.91, 2.69, 19.66, 0.0), (6.72, 1.23, 5.85, 0.0)),
 ]
 
 
 def _figures(path, hw):
-    rows = V.join(path, hw)
     result, _, _, _ = AT.evaluate(path, hw, ks=(1, 10))
     by_k = {r["k"]: r for r in result}
-    assert by_k[10]["mean_regret"] == 0.0
-    return (sum(j.abs_pct for j in rows) / len(rows), by_k[1]["mean_regret"], by_k[1]["max_regret"])
+    rows = V.join(path, hw)
+    return (sum(j.abs_pct for j in rows) / len(rows), by_k[1]["mean_regret"], by_k[1]["max_regret"],
+            by_k[10]["mean_regret"])
 
 
-@pytest.mark.parametrize("name, now, before", CURRENT_FIGURES)
-def test_current_model_figures(tmp_path, name, now, before):
+@pytest.mark.parametrize("name, now, no_mall_write, no_write_overlap", CURRENT_FIGURES)
+def test_current_model_figures(tmp_path, name, now, no_mall_write, no_write_overlap):
     """MAPE and regret of every committed measurement under the current model, and
-    under the same constants with writeOverlapModel switched off; k = 10 finds
-    every shape's best either way. Every set here but held-out 7 and the
-    steady-loop re-measurement was measured before the term existed, so for
-    them this is its in-sample effect."""
+    under the same constants with mallWriteModel, then writeOverlapModel, switched
+    off. Every set here was measured before mallWriteModel existed, so these are
+    its in-sample effects: MAPE lower on 6 of the 12 sets and higher on 5 (mean
+    8.95 against 9.25%); regret at k = 1 worst the same on 11 and lower on the
+    eighth held-out set (19.66 -> 5.85%), mean 2.18 against 2.27% over the 12.
+    Without mallWriteModel the figures are those every held-out set up to the
+    eighth was scored with."""
     import json
     path = os.path.join(ROOT, "data", "measured", name)
     assert _figures(path, CURRENT_HW) == pytest.approx(now, abs=0.01)
     h = json.load(open(CURRENT_HW))
-    assert h["writeOverlapModel"] == 1
-    h["writeOverlapModel"] = 0
-    off = tmp_path / "off.json"
-    off.write_text(json.dumps(h))
-    assert _figures(path, str(off)) == pytest.approx(before, abs=0.01)
+    assert h["mallWriteModel"] == 1 and h["writeOverlapModel"] == 1
+    for key, want in (("mallWriteModel", no_mall_write), ("writeOverlapModel", no_write_overlap)):
+        off = dict(h)
+        off[key] = 0
+        f = tmp_path / ("%s.json" % key)
+        f.write_text(json.dumps(off))
+        assert _figures(path, str(f)) == pytest.approx(want, abs=0.01)
 
 
 def test_best_row_against_hipblaslt_on_every_sweep_shape():
@@ -422,8 +430,9 @@ def test_persistent_tile_term_was_measured_and_is_not_adopted():
         assert t[key] == pytest.approx(measured[key], abs=1e-6)
         # The skeleton K tiles of that run equal the committed calibration's.
         assert measured["persistentStepCycles%d" % i] == pytest.approx(h["persistentStepCycles%d" % i], rel=1e-5)
+    later = ("mallWriteModel", "mallWriteBytesPerSec")  # added to the calibration after that record
     assert {k: v for k, v in t.items() if not k.startswith("persistentTile") and k != "note"} == \
-        {k: v for k, v in h.items() if k != "note"}
+        {k: v for k, v in h.items() if k != "note" and k not in later}
     figures = {}
     for name in ("mi355x.csv", "mi355x-heldout.csv", "mi355x-heldout5.csv"):
         path = os.path.join(ROOT, "data", "measured", name)

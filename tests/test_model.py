@@ -703,6 +703,41 @@ def test_mall_reuse_model_serves_refetches_from_the_mall(tmp_path):
         RM.Hardware(str(bad))
 
 
+def test_mall_write_model_drains_cached_c_into_the_mall(tmp_path):
+    """mallWriteModel 1 with writes at 4 TB/s to HBM and 8 TB/s into the MALL.
+    The last drain of a cached-store row whose A, B and C fit the MALL moves at the
+    MALL's rate, shared by the CUs that hold a workgroup: 2048 x 2048 x 128 in
+    128x128 tiles fills all 256 CUs, so the drain takes half the cycles; 1024 x 2048
+    x 128 holds 128 of them, so each drains at 8 TB/s / 128 against 4 TB/s / 256, a
+    quarter of the cycles. The persistent row stores non-temporally and drains to
+    HBM as before; so does C larger than the MALL. The DRAM-side time is
+    untouched."""
+    base = ', "hbmWriteModel": 1, "hbmWriteBytesPerSec": 4e12'
+    term = ', "mallWriteModel": 1, "mallWriteBytesPerSec": 8e12, "mallBytes": %d'
+    hw = {}
+    for name, extra in (("off", ""), ("on", term % (256 << 20)), ("small", term % 1000000)):
+        f = tmp_path / (name + ".json")
+        f.write_text(_CDNA4_JSON % (base + extra))
+        hw[name] = RM.Hardware(str(f))
+    row = dict(K=128, BM=128, BN=128, BK=64, warpM=64, warpN=64, stages=2, regsPerThread=128)
+    full, half = dict(M=2048, N=2048, **row), dict(M=1024, N=2048, **row)
+    off, on, small = (RM.predict(hw[n], **full) for n in ("off", "on", "small"))
+    assert on["tEpilogueCycles"] == pytest.approx(0.5 * off["tEpilogueCycles"])
+    assert small["tEpilogueCycles"] == pytest.approx(off["tEpilogueCycles"])
+    assert on["hbmTFLOPS"] == pytest.approx(off["hbmTFLOPS"])
+    off, on, small = (RM.predict(hw[n], **half) for n in ("off", "on", "small"))
+    assert off["totalCtas"] == 128.0
+    assert on["tEpilogueCycles"] == pytest.approx(0.25 * off["tEpilogueCycles"])
+    assert small["tEpilogueCycles"] == pytest.approx(off["tEpilogueCycles"])
+    persistent = dict(full, stages=4, schedule=2)
+    assert RM.predict(hw["on"], **persistent)["tEpilogueCycles"] == \
+        pytest.approx(RM.predict(hw["off"], **persistent)["tEpilogueCycles"])
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % (term % (256 << 20)))
+    with pytest.raises(ValueError, match="mallWriteModel 1"):
+        RM.Hardware(str(bad))
+
+
 def test_fill_latency_model_adds_one_wait_per_round(tmp_path):
     """fillLatencyModel 1 with fillLatencySec 1 us: the prediction's time grows by
     one microsecond per round of one-tile-per-workgroup workgroups (fullWaves)
