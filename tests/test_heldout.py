@@ -584,3 +584,30 @@ def test_eighth_heldout_against_hipblaslt():
     slow = sorted(r for r in ratios if r[0] < 1.0)
     assert [r[1] for r in slow] == [(2560, 7168, 5120), (2560, 3584, 5120)]
     assert slow[0][0] == pytest.approx(0.943, abs=0.001)
+
+
+# The ninth held-out sweep (data/sweep/mi355x-heldout9.md).
+REGISTERED9 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout9-registered.csv")
+FROZEN9 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout9-hw.json")
+TABLE9 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout9-table.csv")
+
+
+def test_ninth_heldout_registration():
+    """14 shapes from value sets no earlier set could hold, none in an earlier set;
+    the eighth set's table; the eighth set's constants plus mallWriteModel and its
+    calibrated constant, nothing else changed."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED9)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, REGISTERED6,
+                 REGISTERED7, REGISTERED8, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    values = (1280, 4608, 6656, 9216, 11264)
+    assert len(held) == 14 and not held & earlier
+    assert all(M in values and N in values and K in (640, 1152, 3584, 7680) for M, N, K in held)
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE9) == keys(TABLE8) == list(V.kernel_table_keys())
+    eight, nine = json.load(open(FROZEN8)), json.load(open(FROZEN9))
+    assert nine["mallWriteModel"] == 1 and "mallWriteModel" not in eight
+    assert {k: v for k, v in nine.items() if k not in ("mallWriteModel", "mallWriteBytesPerSec")} == eight
