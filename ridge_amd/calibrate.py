@@ -122,6 +122,13 @@ def band_check(res, spec):
             ok &= check(key, res[key], 0.45 * res["pingPongMfmaCycles"], 2.0 * res["pingPongMfmaCycles"], "cycles",
                         "persistent skeleton K tile: at least its MFMAs")
     for i in (1, 2):
+        key = "pingPongRowStepCycles%d" % i
+        if key in res and "pingPongMfmaCycles" in res:
+            # Both row skeletons issue 64 MFMAs per SIMD per K tile, as the
+            # ping-pong skeleton does; the schedule's waits and refill add to them.
+            ok &= check(key, res[key], 0.9 * res["pingPongMfmaCycles"], 2.0 * res["pingPongMfmaCycles"], "cycles",
+                        "ping-pong row skeleton K tile: at least its MFMAs")
+    for i in (1, 2):
         key, step = "persistentTileCycles%d" % i, "persistentStepCycles%d" % i
         if key in res and step in res:
             # Staging one output tile through LDS and issuing its stores: not
@@ -236,7 +243,8 @@ def hardware_json(res, spec, arch):
     # that reads them switched on) when the log has them.
     for key in (["hbmWriteBytesPerSec", "fillLatencySec", "mallRefillBytesPerSec", "persistentStepCycles1",
                  "persistentStepCycles2", "persistentTileCycles1", "persistentTileCycles2", "launchSeconds",
-                 "launchOverheadSeconds", "launchIsolatedSeconds", "mallWriteBytesPerSec"] +
+                 "launchOverheadSeconds", "launchIsolatedSeconds", "mallWriteBytesPerSec", "pingPongRowStepCycles1",
+                 "pingPongRowStepCycles2"] +
                 ["mallStretchLoad%d" % i for i in range(5)] + ["mallStretch%d" % i for i in range(5)]):
         if key in res:
             out[key] = res[key]
@@ -254,6 +262,7 @@ def hardware_json(res, spec, arch):
                         ("persistentStepModel", ["persistentStepCycles1", "persistentStepCycles2"]),
                         ("launchModel", ["launchOverheadSeconds"]),
                         ("mallWriteModel", ["mallWriteBytesPerSec", "hbmWriteBytesPerSec", "mallRefillBytesPerSec"]),
+                        ("pingPongStepModel", ["pingPongRowStepCycles1", "pingPongRowStepCycles2"]),
                         ("labelModel", ["launchIsolatedSeconds", "hbmWriteBytesPerSec"])):
         if all(k in res for k in needs):
             out[term] = 1

@@ -17,6 +17,8 @@
 #include "cal_common.hpp"
 #include "gemm_mfma.hpp"
 
+#include <string>
+
 using namespace ridgecal;
 
 namespace {
@@ -394,6 +396,112 @@ __global__ __launch_bounds__(((BM / WM) * (BN / WN) + ridge::kPersistentLoaders)
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
 }
 
+// The ping-pong schedule's main loop for one 8-wave table row
+// (gemmMfmaPingPongKernel without its tile order and epilogue): the same two
+// groups of four waves, the same M-phase (refill of the freed stage, fragment
+// reads) and C-phase (the K tile's MFMAs) one phase barrier apart, the same
+// steady ring turns and the same waits. The refill comes from a four-tile
+// L2-resident source laid out as the persistent skeleton's. G K tiles per launch.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void pingPongRowSkeletonKernel(const _Float16* src, int G,
+                                                                                          float* sink, Stamp* out) {
+    using T = ridge::GemmTraits<BM, BN, BK, WM, WN, STAGES, 8>;
+    using Blk = ridge::GemmBlock<BM, BN, BK, WM, WN, STAGES, 8>;
+    static_assert(T::kWaves == 8 && STAGES >= 3, "the ping-pong schedule pairs two groups of four waves");
+    constexpr int TM = T::kTilesM;
+    constexpr int TN = T::kTilesN;
+    constexpr int KS = T::kSteps;
+    constexpr int L = T::kLoadsPerTile;
+    constexpr int kTileBytes = T::kBytesA + T::kBytesB;
+    __shared__ __attribute__((aligned(1024))) char lds[T::kLdsBytes];
+    // One column of tiles, one per workgroup: the block forms its LDS fragment
+    // offsets; its loads are `issue` below, from the four-tile source.
+    Blk blk(lds, src, src, BM * (int)gridDim.x, BN, BK * G);
+    const int wave = blk.wave;
+    const int lane = blk.lane;
+    const int group = wave / 4;
+    uint32_t offA[T::kPerWaveA], offB[T::kPerWaveB];
+#pragma unroll
+    for (int i = 0; i < T::kPerWaveA; ++i) {
+        const int q = ridge::swizzleA<T::kChunksPerRowA>((i * T::kWaves + wave) * 64 + lane);
+        offA[i] = (uint32_t)(((q / T::kChunksPerRowA) * BK + (q % T::kChunksPerRowA) * 8) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < T::kPerWaveB; ++i) {
+        const int q = ridge::swizzleB<T::kChunksPerRowB>((i * T::kWaves + wave) * 64 + lane);
+        offB[i] = (uint32_t)(T::kBytesA + ((q / T::kChunksPerRowB) * BN + (q % T::kChunksPerRowB) * 8) * 2);
+    }
+    auto issue = [&](int g, int stage) {
+        const char* base = reinterpret_cast<const char*>(src) + (g & 3) * kTileBytes;
+        const uint32_t dstA = blk.ldsBase + stage * T::kBytesA;
+        const uint32_t dstB = blk.ldsBase + T::kRegionA + stage * T::kBytesB;
+#pragma unroll
+        for (int i = 0; i < T::kPerWaveA; ++i) ridge::globalLoadLds16(base, offA[i], dstA + (i * T::kWaves + wave) * 1024);
+#pragma unroll
+        for (int i = 0; i < T::kPerWaveB; ++i) ridge::globalLoadLds16(base, offB[i], dstB + (i * T::kWaves + wave) * 1024);
+    };
+    const uint64_t c0 = cycles();
+    const uint64_t r0 = realtime();
+    ridge::staticFor<STAGES - 1>([&](auto sC) {
+        if (sC.value < G) issue(sC.value, sC.value);
+    });
+    if (G >= STAGES - 1) {
+        ridge::waitVmcnt<(STAGES - 2) * L>();
+    } else {
+        ridge::waitVmcnt<0>();
+    }
+    ridge::barrierLds();
+    auto tileBody = [&](auto sC, auto groupC, int kt, bool steady) {
+        constexpr int st = sC.value;
+        constexpr int sRefill = (st + STAGES - 1) % STAGES;
+        constexpr int grp = groupC.value;
+        if (steady) issue(kt + STAGES - 1, sRefill);
+        half8_t fa[KS][TM];
+        half8_t fb[KS][TN];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) blk.template readFrags<st>(ks, fa[ks], fb[ks]);
+        if constexpr (grp == 1) {
+            if (steady) ridge::waitVmcnt<(STAGES - 2) * L>();
+            else ridge::waitVmcnt<0>();
+        }
+        ridge::phaseBarrier();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) blk.mfmaStep(fa[ks], fb[ks]);
+        if constexpr (grp == 0) {
+            if (steady) ridge::waitVmcnt<(STAGES - 2) * L>();
+            else ridge::waitVmcnt<0>();
+        }
+        ridge::phaseBarrier();
+    };
+    auto runGroup = [&](auto groupC) {
+        constexpr int grp = groupC.value;
+        if constexpr (grp == 1) ridge::barrierLds();
+        int kt0 = 0;
+        for (; kt0 + 2 * STAGES - 2 < G; kt0 += STAGES)
+            ridge::staticFor<STAGES>([&](auto sC) { tileBody(sC, groupC, kt0 + sC.value, true); });
+        for (; kt0 < G; kt0 += STAGES)
+            ridge::staticFor<STAGES>([&](auto sC) {
+                const int kt = kt0 + sC.value;
+                if (kt < G) tileBody(sC, groupC, kt, kt + STAGES - 1 < G);
+            });
+        if constexpr (grp == 0) ridge::barrierLds();
+    };
+    if (group == 0) {
+        runGroup(std::integral_constant<int, 0>{});
+    } else {
+        runGroup(std::integral_constant<int, 1>{});
+    }
+    const uint64_t c1 = cycles();
+    const uint64_t r1 = realtime();
+    float acc = 0.0f;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc += blk.acc[tm][tn][0] + blk.acc[tm][tn][3];
+    if (acc == -1.0e38f) sink[0] = acc;
+    if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
+}
+
 constexpr int kPersistentTiles = 1024;  // K tiles per skeleton launch
 
 // Median cycles per K tile of the persistent skeleton over every CU (one
@@ -551,7 +659,63 @@ Curve sweep(const char* label, int cus, uint32_t* dSink, Stamp* dStamps) {
 
 }  // namespace
 
-int main() {
+// Median cycles per K tile of the ping-pong row skeleton over every CU (one
+// workgroup each), and the median clock.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+double pingPongRowCycles(int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, double& clockHz) {
+    auto k = pingPongRowSkeletonKernel<BM, BN, BK, WM, WN, STAGES>;
+    hipLaunchKernelGGL(k, dim3(cus), dim3((BM / WM) * (BN / WN) * 64), 0, nullptr, dSrc, kPersistentTiles, dSink,
+                       dStamps);
+    CAL_HIP_CHECK(hipGetLastError());
+    CAL_HIP_CHECK(hipDeviceSynchronize());
+    std::vector<Stamp> st(cus);
+    CAL_HIP_CHECK(hipMemcpy(st.data(), dStamps, cus * sizeof(Stamp), hipMemcpyDeviceToHost));
+    double cyc = 0.0;
+    medianStamps(st, cyc, clockHz);
+    return cyc / kPersistentTiles;
+}
+
+// One ping-pong row's cycles per K tile (the median of kRepeats launches),
+// reported as `key`.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+double pingPongRowStep(const char* key, int cus, const _Float16* dSrc, float* dSink, Stamp* dStamps, bool& ok) {
+    std::vector<double> reps;
+    double hz = 0.0;
+    for (int r = 0; r < kRepeats; ++r) reps.push_back(pingPongRowCycles<BM, BN, BK, WM, WN, STAGES>(cus, dSrc, dSink,
+                                                                                                    dStamps, hz));
+    const double t = middle(reps);
+    std::printf("  %dx%dx%d w%dx%d s%d: %.1f cycles per K tile at %.1f MHz\n", BM, BN, BK, WM, WN, STAGES, t,
+                hz / 1e6);
+    ok &= reportConstant(key, t, "cycles", reps);
+    std::printf("CAL_INFO %sClockHz %.6e\n", key, hz);
+    std::printf("CAL_RESULT %s %.6f\n", key, t);
+    return t;
+}
+
+// The ping-pong row skeletons of the two classes of the table's ping-pong rows:
+// BK = 32 with 128x64 (or 64x128) wave tiles, and BK = 64 with 64x64 ones.
+bool pingPongRows(int cus, float* dSink, Stamp* dStamps, const std::vector<uint32_t>& hOperands) {
+    std::printf("\nping-pong row skeletons: the kernel's phase loop on a four-tile L2-resident source, %d K tiles\n",
+                kPersistentTiles);
+    _Float16* dSrc = nullptr;
+    constexpr size_t kSrcBytes = 4 * 48 * 1024;
+    CAL_HIP_CHECK(hipMalloc(&dSrc, kSrcBytes));
+    for (size_t off = 0; off < kSrcBytes; off += 16 * 1024)
+        CAL_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(dSrc) + off, hOperands.data(), 16 * 1024,
+                                hipMemcpyHostToDevice));
+    bool ok = true;
+    pingPongRowStep<256, 256, 32, 128, 64, 3>("pingPongRowStepCycles1", cus, dSrc, dSink, dStamps, ok);
+    pingPongRowStep<256, 128, 64, 64, 64, 3>("pingPongRowStepCycles2", cus, dSrc, dSink, dStamps, ok);
+    CAL_HIP_CHECK(hipFree(dSrc));
+    return ok;
+}
+
+int main(int argc, char** argv) {
+    const bool pingPongOnly = argc > 1 && std::string(argv[1]) == "--ping-pong-rows-only";
+    if (argc > 1 && !pingPongOnly) {
+        std::fprintf(stderr, "usage: cal-smem-bw [--ping-pong-rows-only]\n");
+        return 2;
+    }
     const hipDeviceProp_t prop = deviceBanner();
     const int cus = prop.multiProcessorCount;
     uint32_t* dSink = nullptr;
@@ -559,6 +723,15 @@ int main() {
     CAL_HIP_CHECK(hipMalloc(&dSink, sizeof(uint32_t)));
     CAL_HIP_CHECK(hipMalloc(&dStamps, cus * sizeof(Stamp)));
     warmUp();
+    if (pingPongOnly) {
+        float* dFSink = nullptr;
+        CAL_HIP_CHECK(hipMalloc(&dFSink, sizeof(float)));
+        const bool ok = pingPongRows(cus, dFSink, dStamps, randomHalfWords());
+        CAL_HIP_CHECK(hipFree(dFSink));
+        CAL_HIP_CHECK(hipFree(dSink));
+        CAL_HIP_CHECK(hipFree(dStamps));
+        return ok ? 0 : 1;
+    }
     const Curve ctl = sweep<kPatLinear>("control: linear ds_read_b128 (conflict-free)", cus, dSink, dStamps);
     const Curve a = sweep<kPatA>("A fragments: ds_read_b128 on the swizzled A tile", cus, dSink, dStamps);
     const Curve b = sweep<kPatB>("B fragments: ds_read_b64_tr_b16 on the swizzled B tile", cus, dSink, dStamps);
@@ -695,6 +868,7 @@ int main() {
     persistentTileCost<256, 128, 32, 64, 64, 6>("persistentTileCycles2", cus, dSrc, dFSink, dStamps, dC, ok);
     CAL_HIP_CHECK(hipFree(dC));
     CAL_HIP_CHECK(hipFree(dSrc));
+    ok &= pingPongRows(cus, dFSink, dStamps, hOperands);
     CAL_HIP_CHECK(hipFree(dOperands));
     CAL_HIP_CHECK(hipFree(dRefill));
     CAL_HIP_CHECK(hipFree(dFSink));

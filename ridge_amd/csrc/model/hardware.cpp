@@ -125,6 +125,8 @@ std::vector<KeyRule> schemaFor(HardwareModel& h) {
         R("persistentTileCycles2", h.persistentTileCycles[1]),
         I("fillShareModel", h.fillShareModel), I("mallReuseModel", h.mallReuseModel), R("mallBytes", h.mallBytes),
         I("mallWriteModel", h.mallWriteModel), R("mallWriteBytesPerSec", h.mallWriteBytesPerSec),
+        I("pingPongStepModel", h.pingPongStepModel), R("pingPongRowStepCycles1", h.pingPongRowStepCycles[0]),
+        R("pingPongRowStepCycles2", h.pingPongRowStepCycles[1]),
         I("launchModel", h.launchModel), R("launchOverheadSeconds", h.launchOverheadSeconds),
         R("launchIsolatedSeconds", h.launchIsolatedSeconds), I("labelModel", h.labelModel),
         R("nominalClockHz", h.nominalClockHz),
@@ -181,6 +183,7 @@ std::string inconsistency(const HardwareModel& h) {
         {"persistentStepModel", h.persistentStepModel, 1}, {"persistentTileModel", h.persistentTileModel, 1},
         {"fillShareModel", h.fillShareModel, 1},
         {"mallReuseModel", h.mallReuseModel, 1}, {"mallWriteModel", h.mallWriteModel, 1},
+        {"pingPongStepModel", h.pingPongStepModel, 1},
         {"launchModel", h.launchModel, 1},
         {"labelModel", h.labelModel, 2},
     };
@@ -221,6 +224,10 @@ std::string inconsistency(const HardwareModel& h) {
     if (h.mallWriteModel == 1 && !(h.hbmWriteModel == 1 && h.mallWriteBytesPerSec > 0.0 && h.mallBytes > 0.0))
         return "mallWriteModel 1 refines hbmWriteModel 1 and reads mallWriteBytesPerSec and mallBytes, which must be "
                "positive";
+    if (h.pingPongStepModel == 1 &&
+        !(h.pingPongModel == 1 && h.pingPongRowStepCycles[0] > 0.0 && h.pingPongRowStepCycles[1] > 0.0))
+        return "pingPongStepModel 1 refines pingPongModel 1 and reads pingPongRowStepCycles1 and "
+               "pingPongRowStepCycles2, which must be positive";
     if (h.persistentStepModel == 1 && !(h.persistentStepCycles[0] > 0.0 && h.persistentStepCycles[1] > 0.0))
         return "persistentStepModel 1 reads persistentStepCycles1 and persistentStepCycles2, which must be positive";
     if (h.persistentTileModel == 1 && !(h.persistentTileCycles[0] >= 0.0 && h.persistentTileCycles[1] >= 0.0 &&

@@ -67,6 +67,10 @@
 //   write overlap         = hw.writeOverlapModel 1: C's writes to DRAM overlap
 //                           the tile loads the L2s serve; the DRAM reads come
 //                           before both (reference: one DRAM stream)
+//   ping-pong K-step      = hw.pingPongStepModel 1: a ping-pong row's max(compute,
+//                           operand reads) scaled by the measured/modelled ratio
+//                           of the ping-pong row skeleton of its class (BK 32 or
+//                           64) (reference: no ping-pong schedule)
 //   MALL drain            = hw.mallWriteModel 1: the last drain of cached C
 //                           stores goes to the MALL when A, B and C fit it, at
 //                           the MALL's write rate shared by the CUs holding a
@@ -259,6 +263,23 @@ double persistentStepRatio(const GemmConfig& cfg, const HardwareModel& hw, int d
     return hw.persistentStepCycles[two ? 1 : 0] / (tC + tS);
 }
 
+// pingPongStepModel 1: the measured K-step of the ping-pong row skeleton of a
+// row's class (its BK) over the model's max(MFMAs, reads) for the skeleton's
+// own row. The skeletons are cal-smem-bw's: 256x256x32 w128x64 s3 and
+// 256x128x64 w64x64 s3, the kernel's phase loop on an L2-resident source.
+double pingPongStepRatio(const GemmConfig& cfg, const HardwareModel& hw, int db) {
+    GemmConfig skel = cfg;
+    const bool deep = cfg.BK >= 64;
+    skel.BM = 256;
+    skel.BN = deep ? 128 : 256;
+    skel.BK = deep ? 64 : 32;
+    skel.warpM = deep ? 64 : 128;
+    skel.warpN = 64;
+    double tC = 0.0, tS = 0.0;
+    stepParts(skel, hw, db, tC, tS);
+    return hw.pingPongRowStepCycles[deep ? 1 : 0] / std::max(tC, tS);
+}
+
 }  // namespace
 
 Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
@@ -293,6 +314,9 @@ Prediction predictCore(const GemmConfig& cfgIn, const HardwareModel& hw) {
     const bool derivedPingPong = hw.simdsPerSM > 0 && numWarps == 2 * hw.simdsPerSM && cfg.stages >= 3;
     const bool pingPong = hw.pingPongModel == 1 && (cfg.schedule < 0 ? derivedPingPong : cfg.schedule == 1);
     double tStep = pingPong ? std::max(tCompute, tSmem) : tCompute + tSmem;
+    // The row skeleton of the same class (BK) runs the schedule's barriers,
+    // waits and refill writes, which the max leaves out.
+    if (pingPong && hw.pingPongStepModel == 1) tStep *= pingPongStepRatio(cfg, hw, db);
     // uniformOverlapModel 1: two compute waves per SIMD that run the uniform
     // schedule (the 8-wave uniform rows, and the 8-compute-wave persistent rows,
     // whose compute waves run the same loop with one barrier per K tile) hide

@@ -344,21 +344,35 @@ CURRENT_HW = os.path.join(ROOT, "data", "hardware", "mi355x.json")
 # model every held-out set up to the eighth was scored against), and with its
 # writeOverlapModel switched off.
 CURRENT_FIGURES = [
-    ("mi355x.csv", (7.69, 1.19, 6.57, 0.0), (8.93, 1.19, 6.57, 0.0), (8.72, 3.24, 12.63, 0.30)),
-    ("mi355x-replicate.csv", (8.08, 1.02, 8.86, 0.0), (8.41, 1.02, 8.86, 0.0), (8.65, 4.20, 18.54, 0.07)),
-    ("mi355x-baseline-configs.csv", (11.46, 9.91, 27.95, 0.0), (12.68, 9.91, 27.95, 0.0),
-     (13.50, 14.32, 27.95, 0.0)),
-    ("mi355x-heldout.csv", (8.81, 1.41, 11.04, 0.0), (7.64, 1.38, 11.04, 0.0), (8.73, 1.42, 11.04, 0.55)),
-    ("mi355x-heldout2.csv", (11.61, 2.20, 8.22, 0.0), (11.33, 2.00, 8.22, 0.0), (11.37, 3.36, 10.50, 0.0)),
-    ("mi355x-heldout3.csv", (8.11, 0.50, 4.19, 0.0), (8.41, 0.50, 4.19, 0.0), (9.84, 4.16, 23.38, 0.06)),
-    ("mi355x-heldout4.csv", (11.48, 1.98, 13.04, 0.0), (10.10, 1.87, 13.04, 0.0), (11.36, 1.98, 13.04, 0.0)),
-    ("mi355x-heldout5.csv", (8.28, 1.88, 12.23, 0.0), (8.04, 1.88, 12.23, 0.0), (8.30, 2.38, 12.23, 0.0)),
-    ("mi355x-heldout6.csv", (8.74, 2.01, 15.43, 0.0), (8.18, 2.01, 15.43, 0.0), (9.34, 2.15, 15.43, 0.12)),
-    ("mi355x-heldout7.csv", (8.65, 2.08, 10.16, 0.0), (9.26, 2.08, 10.16, 0.0), (8.17, 2.55, 10.16, 0.0)),
+    # (set, now, without pingPongStepModel, without mallWriteModel, without
+    # writeOverlapModel); each figure is (MAPE, k = 1 mean, k = 1 worst, k = 10 mean).
+    ("mi355x.csv", (7.20, 1.19, 6.57, 0.0), (7.69, 1.19, 6.57, 0.0), (8.71, 1.85, 12.14, 0.0),
+     (8.23, 3.24, 12.63, 0.30)),
+    ("mi355x-replicate.csv", (7.45, 1.02, 8.86, 0.0), (8.08, 1.02, 8.86, 0.0), (7.96, 1.64, 8.86, 0.0),
+     (8.02, 4.20, 18.54, 0.07)),
+    ("mi355x-baseline-configs.csv", (10.64, 9.91, 27.95, 0.0), (11.46, 9.91, 27.95, 0.0),
+     (12.28, 9.91, 27.95, 0.0), (12.68, 14.32, 27.95, 0.0)),
+    ("mi355x-heldout.csv", (8.04, 1.41, 11.04, 0.0), (8.81, 1.41, 11.04, 0.0), (7.20, 2.35, 13.59, 0.0),
+     (7.95, 1.42, 11.04, 0.55)),
+    ("mi355x-heldout2.csv", (11.01, 2.20, 8.22, 0.0), (11.61, 2.20, 8.22, 0.0), (11.08, 1.53, 8.22, 0.0),
+     (10.77, 3.36, 10.50, 0.0)),
+    ("mi355x-heldout3.csv", (7.44, 0.50, 4.19, 0.0), (8.11, 0.50, 4.19, 0.0), (7.91, 0.50, 4.19, 0.0),
+     (9.17, 4.16, 23.38, 0.06)),
+    ("mi355x-heldout4.csv", (10.67, 1.98, 13.04, 0.0), (11.48, 1.98, 13.04, 0.0), (9.43, 1.52, 13.04, 0.0),
+     (10.55, 1.98, 13.04, 0.0)),
+    ("mi355x-heldout5.csv", (7.58, 1.88, 12.23, 0.0), (8.28, 1.88, 12.23, 0.0), (7.43, 1.88, 12.23, 0.0),
+     (7.61, 2.38, 12.23, 0.0)),
+    ("mi355x-heldout6.csv", (7.99, 2.01, 15.43, 0.0), (8.74, 2.01, 15.43, 0.0), (7.66, 2.53, 15.43, 0.0),
+     (8.59, 2.15, 15.43, 0.12)),
+    ("mi355x-heldout7.csv", (8.12, 0.13, 1.83, 0.0), (8.65, 2.08, 10.16, 0.0), (9.03, 2.79, 20.01, 0.0),
+     (7.64, 0.99, 11.03, 0.0)),
     # The in-sample shapes re-measured with the steady-pass kernels.
-    ("mi355x-steady-loop.csv", (7.30, 0.70, 5.92, 0.0), (9.07, 0.70, 5.92, 0.0), (7.99, 3.39, 15.05, 0.05)),
-    ("mi355x-heldout8.csv", (7.20, 1.23, 5.85, 0.0), (8.91, 2.69, 19.66, 0.0), (6.72, 1.23, 5.85, 0.0)),
-    ("mi355x-heldout9.csv", (6.95, 1.98, 11.37, 0.0), (7.60, 2.34, 11.37, 0.0), (6.78, 2.46, 11.37, 0.20)),
+    ("mi355x-steady-loop.csv", (6.84, 0.70, 5.92, 0.0), (7.30, 0.70, 5.92, 0.0), (8.95, 1.51, 11.40, 0.0),
+     (7.54, 3.39, 15.05, 0.05)),
+    ("mi355x-heldout8.csv", (7.18, 0.67, 5.17, 0.0), (7.20, 1.23, 5.85, 0.0), (9.10, 2.55, 19.66, 0.0),
+     (6.69, 0.67, 5.17, 0.0)),
+    ("mi355x-heldout9.csv", (6.50, 1.17, 4.83, 0.0), (6.95, 1.98, 11.37, 0.0), (7.62, 1.52, 5.28, 0.0),
+     (6.33, 1.65, 6.95, 0.20)),
 ]
 
 
@@ -370,22 +384,25 @@ def _figures(path, hw):
             by_k[10]["mean_regret"])
 
 
-@pytest.mark.parametrize("name, now, no_mall_write, no_write_overlap", CURRENT_FIGURES)
-def test_current_model_figures(tmp_path, name, now, no_mall_write, no_write_overlap):
+@pytest.mark.parametrize("name, now, no_ping_pong_step, no_mall_write, no_write_overlap", CURRENT_FIGURES)
+def test_current_model_figures(tmp_path, name, now, no_ping_pong_step, no_mall_write, no_write_overlap):
     """MAPE and regret of every committed measurement under the current model, and
-    under the same constants with mallWriteModel, then writeOverlapModel, switched
-    off. Every set but the ninth held-out one was measured before mallWriteModel
-    existed, so for them these are its in-sample effects: MAPE lower on 6 of the 12 sets and higher on 5 (mean
-    8.95 against 9.25%); regret at k = 1 worst the same on 11 and lower on the
-    eighth held-out set (19.66 -> 5.85%), mean 2.18 against 2.27% over the 12.
-    Without mallWriteModel the figures are those every held-out set up to the
-    eighth was scored with."""
+    under the same constants with pingPongStepModel, mallWriteModel, then
+    writeOverlapModel switched off (one at a time).
+
+    Every set was measured before pingPongStepModel existed, so for all 13 these are
+    its in-sample effects: MAPE lower on every set (mean 8.20 against 8.80%); regret
+    at k = 1 worst lower on the seventh, eighth and ninth held-out sets (10.16 ->
+    1.83, 5.85 -> 5.17, 11.37 -> 4.83%) and the same on the other 10. Without
+    pingPongStepModel the figures are those the ninth held-out set was scored with;
+    without it and mallWriteModel, those of every held-out set up to the eighth."""
     import json
     path = os.path.join(ROOT, "data", "measured", name)
     assert _figures(path, CURRENT_HW) == pytest.approx(now, abs=0.01)
     h = json.load(open(CURRENT_HW))
-    assert h["mallWriteModel"] == 1 and h["writeOverlapModel"] == 1
-    for key, want in (("mallWriteModel", no_mall_write), ("writeOverlapModel", no_write_overlap)):
+    assert h["pingPongStepModel"] == 1 and h["mallWriteModel"] == 1 and h["writeOverlapModel"] == 1
+    for key, want in (("pingPongStepModel", no_ping_pong_step), ("mallWriteModel", no_mall_write),
+                      ("writeOverlapModel", no_write_overlap)):
         off = dict(h)
         off[key] = 0
         f = tmp_path / ("%s.json" % key)
@@ -431,7 +448,9 @@ def test_persistent_tile_term_was_measured_and_is_not_adopted():
         assert t[key] == pytest.approx(measured[key], abs=1e-6)
         # The skeleton K tiles of that run equal the committed calibration's.
         assert measured["persistentStepCycles%d" % i] == pytest.approx(h["persistentStepCycles%d" % i], rel=1e-5)
-    later = ("mallWriteModel", "mallWriteBytesPerSec")  # added to the calibration after that record
+    # Added to the calibration after that record.
+    later = ("mallWriteModel", "mallWriteBytesPerSec", "pingPongStepModel", "pingPongRowStepCycles1",
+             "pingPongRowStepCycles2")
     assert {k: v for k, v in t.items() if not k.startswith("persistentTile") and k != "note"} == \
         {k: v for k, v in h.items() if k != "note" and k not in later}
     figures = {}

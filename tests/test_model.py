@@ -796,6 +796,44 @@ def test_persistent_step_model_scales_by_the_skeleton_of_the_class(tmp_path):
         RM.Hardware(str(bad))
 
 
+def test_ping_pong_step_model_scales_by_the_row_skeleton_of_the_class(tmp_path):
+    """pingPongStepModel 1 on the placeholders (4 cycles per MFMA per CU, one
+    blended 128 B/cycle LDS rate, four SIMDs). The skeleton rows' own
+    max(MFMAs, reads):
+      256x256x32 w128x64: tC = 32 MFMAs x 8 waves x 4 = 1024, tS = 8 x (128 + 64)
+        x 32 x 2 B / 128 = 768: 1024 cycles;
+      256x128x64 w64x64: tC = 32 x 8 x 4 = 1024, tS = 8 x 128 x 64 x 2 / 128 =
+        1024: 1024 cycles.
+    With measured K tiles of 1100 and 1300 cycles, a BK = 32 ping-pong row's
+    K-step is scaled by 1100/1024 and a BK = 64 one's by 1300/1024: 256x256x64
+    w128x64 s3 has tC = 64 x 8 x 4 = 2048 and tS = 8 x 192 x 64 x 2 / 128 =
+    1536, so 2048 x 1300 / 1024 = 2600. Rows of four waves keep their K-step
+    (256x128x64 w128x64: tC = 64 x 4 x 4 = 1024 plus tS = 4 x 192 x 64 x 2 / 128
+    = 768, 1792 cycles), and the term needs pingPongModel 1 (the gfx950 preset's
+    default)."""
+    extra = ', "simdsPerSM": 4, "pingPongModel": 1%s'
+    on = tmp_path / "on.json"
+    on.write_text(_CDNA4_JSON % (extra % ', "pingPongStepModel": 1, "pingPongRowStepCycles1": 1100, '
+                                          '"pingPongRowStepCycles2": 1300'))
+    off = tmp_path / "off.json"
+    off.write_text(_CDNA4_JSON % (extra % ""))
+    hw_on, hw_off = RM.Hardware(str(on)), RM.Hardware(str(off))
+    row = dict(M=8192, N=8192, K=4096, regsPerThread=128, groupM=4)
+    for tile, want_off, want_on in (
+            (dict(BM=256, BN=256, BK=32, warpM=128, warpN=64, stages=3), 1024.0, 1100.0),
+            (dict(BM=256, BN=256, BK=32, warpM=64, warpN=128, stages=4), 1024.0, 1100.0),
+            (dict(BM=256, BN=128, BK=64, warpM=64, warpN=64, stages=3), 1024.0, 1300.0),
+            (dict(BM=256, BN=256, BK=64, warpM=128, warpN=64, stages=3), 2048.0, 2600.0),
+            (dict(BM=256, BN=128, BK=64, warpM=128, warpN=64, stages=3), 1792.0, 1792.0)):
+        assert RM.predict(hw_off, **row, **tile)["tStepCycles"] == pytest.approx(want_off)
+        assert RM.predict(hw_on, **row, **tile)["tStepCycles"] == pytest.approx(want_on)
+    bad = tmp_path / "bad.json"
+    bad.write_text(_CDNA4_JSON % ', "simdsPerSM": 4, "pingPongModel": 0, "pingPongStepModel": 1, '
+                                 '"pingPongRowStepCycles1": 1100, "pingPongRowStepCycles2": 1300')
+    with pytest.raises(ValueError, match="pingPongStepModel 1"):
+        RM.Hardware(str(bad))
+
+
 def test_persistent_tile_model_charges_the_epilogue_between_tiles(tmp_path):
     """persistentTileModel 1 on the placeholders, with skeleton K tiles equal to the
     rows' own reads + MFMAs (1024 cycles each, so the step ratio is 1) and
