@@ -668,3 +668,31 @@ def test_ninth_heldout_figures_as_reported():
     xs = [x for x, _, _ in ratios]
     assert len(xs) == 14 and min(xs) > 1.0
     assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.100, abs=0.001)
+
+
+# The tenth held-out sweep (data/sweep/mi355x-heldout10.md).
+REGISTERED10 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout10-registered.csv")
+FROZEN10 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout10-hw.json")
+TABLE10 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout10-table.csv")
+
+
+def test_tenth_heldout_registration():
+    """14 shapes from value sets no earlier set could hold, none in an earlier set;
+    the ninth set's table; the ninth set's constants plus pingPongStepModel and its
+    two calibrated skeleton K tiles, nothing else changed."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED10)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, REGISTERED6,
+                 REGISTERED7, REGISTERED8, REGISTERED9, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    values = (1792, 5632, 7680, 8704, 13312)
+    assert len(held) == 14 and not held & earlier
+    assert all(M in values and N in values and K in (896, 1920, 2816, 4864) for M, N, K in held)
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE10) == keys(TABLE9) == list(V.kernel_table_keys())
+    nine, ten = json.load(open(FROZEN9)), json.load(open(FROZEN10))
+    added = ("pingPongStepModel", "pingPongRowStepCycles1", "pingPongRowStepCycles2")
+    assert ten["pingPongStepModel"] == 1 and not any(k in nine for k in added)
+    assert {k: v for k, v in ten.items() if k not in added} == nine
