@@ -692,6 +692,26 @@ double pingPongRowStep(const char* key, int cus, const _Float16* dSrc, float* dS
     return t;
 }
 
+// The persistent skeleton of the table's BK = 128 rows (one compute wave per
+// SIMD, 128x64x128 w64x32 s3), reported as persistentStepCycles3: a record the
+// model does not read, run only by --persistent-bk128-only. Its 48 KiB refill per
+// K tile from the L2s bounds it: the reads alone and the MFMAs alone both take
+// about 827 cycles, and the combined figure spreads 7% from launch to launch.
+bool persistentDeep(int cus, float* dSink, Stamp* dStamps, const std::vector<uint32_t>& hOperands) {
+    std::printf("\npersistent skeleton of the BK = 128 rows: compute waves + 2 loader waves, %d K tiles\n",
+                kPersistentTiles);
+    _Float16* dSrc = nullptr;
+    constexpr size_t kSrcBytes = 4 * 48 * 1024;
+    CAL_HIP_CHECK(hipMalloc(&dSrc, kSrcBytes));
+    for (size_t off = 0; off < kSrcBytes; off += 16 * 1024)
+        CAL_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(dSrc) + off, hOperands.data(), 16 * 1024,
+                                hipMemcpyHostToDevice));
+    bool ok = true;
+    persistentStep<128, 64, 128, 64, 32, 3>("persistentStepCycles3", cus, dSrc, dSink, dStamps, ok);
+    CAL_HIP_CHECK(hipFree(dSrc));
+    return ok;
+}
+
 // The ping-pong row skeletons of the two classes of the table's ping-pong rows:
 // BK = 32 with 128x64 (or 64x128) wave tiles, and BK = 64 with 64x64 ones.
 bool pingPongRows(int cus, float* dSink, Stamp* dStamps, const std::vector<uint32_t>& hOperands) {
@@ -712,8 +732,9 @@ bool pingPongRows(int cus, float* dSink, Stamp* dStamps, const std::vector<uint3
 
 int main(int argc, char** argv) {
     const bool pingPongOnly = argc > 1 && std::string(argv[1]) == "--ping-pong-rows-only";
-    if (argc > 1 && !pingPongOnly) {
-        std::fprintf(stderr, "usage: cal-smem-bw [--ping-pong-rows-only]\n");
+    const bool deepOnly = argc > 1 && std::string(argv[1]) == "--persistent-bk128-only";
+    if (argc > 1 && !pingPongOnly && !deepOnly) {
+        std::fprintf(stderr, "usage: cal-smem-bw [--ping-pong-rows-only | --persistent-bk128-only]\n");
         return 2;
     }
     const hipDeviceProp_t prop = deviceBanner();
@@ -723,10 +744,11 @@ int main(int argc, char** argv) {
     CAL_HIP_CHECK(hipMalloc(&dSink, sizeof(uint32_t)));
     CAL_HIP_CHECK(hipMalloc(&dStamps, cus * sizeof(Stamp)));
     warmUp();
-    if (pingPongOnly) {
+    if (pingPongOnly || deepOnly) {
         float* dFSink = nullptr;
         CAL_HIP_CHECK(hipMalloc(&dFSink, sizeof(float)));
-        const bool ok = pingPongRows(cus, dFSink, dStamps, randomHalfWords());
+        const bool ok = pingPongOnly ? pingPongRows(cus, dFSink, dStamps, randomHalfWords())
+                                     : persistentDeep(cus, dFSink, dStamps, randomHalfWords());
         CAL_HIP_CHECK(hipFree(dFSink));
         CAL_HIP_CHECK(hipFree(dSink));
         CAL_HIP_CHECK(hipFree(dStamps));
