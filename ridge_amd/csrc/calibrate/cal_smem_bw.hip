@@ -502,6 +502,109 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void pingPongRowSkeleto
     if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
 }
 
+// The uniform schedule's main loop for one table row (gemmMfmaKernel without
+// its tile order, K stagger and epilogue): the same prologue, fragment buffers
+// alternating per k-step, one wait and one barrier per K tile, the refill of the
+// freed stage after the barrier, and the steady passes where the kernel has them
+// (rows of at most four waves). The refill comes from a four-tile L2-resident
+// source laid out as the persistent skeleton's. G K tiles per launch; the host
+// launches one or more workgroups per CU.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void uniformRowSkeletonKernel(const _Float16* src, int G,
+                                                                                         float* sink, Stamp* out) {
+    using T = ridge::GemmTraits<BM, BN, BK, WM, WN, STAGES, 8>;
+    using Blk = ridge::GemmBlock<BM, BN, BK, WM, WN, STAGES, 8>;
+    constexpr int TM = T::kTilesM;
+    constexpr int TN = T::kTilesN;
+    constexpr int KS = T::kSteps;
+    constexpr int L = T::kLoadsPerTile;
+    constexpr int kTileBytes = T::kBytesA + T::kBytesB;
+    __shared__ __attribute__((aligned(1024))) char lds[T::kLdsBytes];
+    Blk blk(lds, src, src, BM * (int)gridDim.x, BN, BK * G);
+    const int wave = blk.wave;
+    const int lane = blk.lane;
+    uint32_t offA[T::kPerWaveA], offB[T::kPerWaveB];
+#pragma unroll
+    for (int i = 0; i < T::kPerWaveA; ++i) {
+        const int q = ridge::swizzleA<T::kChunksPerRowA>((i * T::kWaves + wave) * 64 + lane);
+        offA[i] = (uint32_t)(((q / T::kChunksPerRowA) * BK + (q % T::kChunksPerRowA) * 8) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < T::kPerWaveB; ++i) {
+        const int q = ridge::swizzleB<T::kChunksPerRowB>((i * T::kWaves + wave) * 64 + lane);
+        offB[i] = (uint32_t)(T::kBytesA + ((q / T::kChunksPerRowB) * BN + (q % T::kChunksPerRowB) * 8) * 2);
+    }
+    auto issue = [&](int g, int stage) {
+        const char* base = reinterpret_cast<const char*>(src) + (g & 3) * kTileBytes;
+        const uint32_t dstA = blk.ldsBase + stage * T::kBytesA;
+        const uint32_t dstB = blk.ldsBase + T::kRegionA + stage * T::kBytesB;
+#pragma unroll
+        for (int i = 0; i < T::kPerWaveA; ++i) ridge::globalLoadLds16(base, offA[i], dstA + (i * T::kWaves + wave) * 1024);
+#pragma unroll
+        for (int i = 0; i < T::kPerWaveB; ++i) ridge::globalLoadLds16(base, offB[i], dstB + (i * T::kWaves + wave) * 1024);
+    };
+    const int numK = G;
+    const uint64_t c0 = cycles();
+    const uint64_t r0 = realtime();
+    ridge::staticFor<STAGES>([&](auto sC) {
+        if (sC.value < numK) issue(sC.value, sC.value);
+    });
+    if (numK >= STAGES) {
+        ridge::waitVmcnt<(STAGES - 1) * L>();
+    } else {
+        ridge::waitVmcnt<0>();
+    }
+    ridge::barrierLds();
+    half8_t fa[2][TM];
+    half8_t fb[2][TN];
+    blk.template readFrags<0>(0, fa[0], fb[0]);
+    constexpr int U = (STAGES * KS) % 2 == 0 ? STAGES : 2 * STAGES;
+    auto pass = [&](int kt0, auto steadyC) {
+        constexpr bool steady = steadyC.value;
+        ridge::staticFor<U>([&](auto iC) {
+            constexpr int i = iC.value;
+            constexpr int st = i % STAGES;
+            constexpr int sNext = (st + 1) % STAGES;
+            const int kt = kt0 + i;
+            if (steady || kt < numK) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int cur = (i * KS + ks) & 1;
+                    if (ks + 1 < KS) {
+                        blk.template readFrags<st>(ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                    } else if (steady || kt + 1 < numK) {
+                        if (steady || kt + STAGES - 1 < numK) {
+                            ridge::waitVmcnt<(STAGES - 2) * L>();
+                        } else {
+                            ridge::waitVmcnt<0>();
+                        }
+                        ridge::barrierLds();
+                        if (steady || kt + STAGES < numK) issue(kt + STAGES, st);
+                        blk.template readFrags<sNext>(0, fa[cur ^ 1], fb[cur ^ 1]);
+                    }
+                    blk.mfmaStep(fa[cur], fb[cur]);
+                    ridge::interleaveHint<TM, TN>();
+                }
+            }
+        });
+    };
+    int kt0 = 0;
+    if constexpr (T::kWaves <= 4) {
+        for (; kt0 + U - 1 + STAGES < numK; kt0 += U) pass(kt0, std::true_type{});
+    }
+    for (; kt0 < numK; kt0 += U) pass(kt0, std::false_type{});
+    ridge::barrierLds();
+    const uint64_t c1 = cycles();
+    const uint64_t r1 = realtime();
+    float acc = 0.0f;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc += blk.acc[tm][tn][0] + blk.acc[tm][tn][3];
+    if (acc == -1.0e38f) sink[0] = acc;
+    if (threadIdx.x == 0) out[blockIdx.x] = Stamp{c0, c1, r0, r1};
+}
+
 constexpr int kPersistentTiles = 1024;  // K tiles per skeleton launch
 
 // Median cycles per K tile of the persistent skeleton over every CU (one
@@ -692,6 +795,65 @@ double pingPongRowStep(const char* key, int cus, const _Float16* dSrc, float* dS
     return t;
 }
 
+// Median cycles per K tile of the uniform row skeleton with perCu workgroups on
+// every CU (all resident at once), and the median clock.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+double uniformRowCycles(int cus, int perCu, const _Float16* dSrc, float* dSink, Stamp* dStamps, double& clockHz) {
+    auto k = uniformRowSkeletonKernel<BM, BN, BK, WM, WN, STAGES>;
+    const int blocks = cus * perCu;
+    hipLaunchKernelGGL(k, dim3(blocks), dim3((BM / WM) * (BN / WN) * 64), 0, nullptr, dSrc, kPersistentTiles, dSink,
+                       dStamps);
+    CAL_HIP_CHECK(hipGetLastError());
+    CAL_HIP_CHECK(hipDeviceSynchronize());
+    std::vector<Stamp> st(blocks);
+    CAL_HIP_CHECK(hipMemcpy(st.data(), dStamps, blocks * sizeof(Stamp), hipMemcpyDeviceToHost));
+    double cyc = 0.0;
+    medianStamps(st, cyc, clockHz);
+    return cyc / kPersistentTiles;
+}
+
+// One uniform row's cycles per K tile of each workgroup (the median of kRepeats
+// launches), reported as `key`.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES>
+void uniformRowStep(const char* key, int cus, int perCu, const _Float16* dSrc, float* dSink, Stamp* dStamps,
+                    bool& ok) {
+    std::vector<double> reps;
+    double hz = 0.0;
+    for (int r = 0; r < kRepeats; ++r)
+        reps.push_back(uniformRowCycles<BM, BN, BK, WM, WN, STAGES>(cus, perCu, dSrc, dSink, dStamps, hz));
+    const double t = middle(reps);
+    std::printf("  %dx%dx%d w%dx%d s%d, %d per CU: %.1f cycles per K tile of each workgroup at %.1f MHz\n", BM, BN,
+                BK, WM, WN, STAGES, perCu, t, hz / 1e6);
+    ok &= reportConstant(key, t, "cycles", reps);
+    std::printf("CAL_INFO %sClockHz %.6e\n", key, hz);
+    std::printf("CAL_RESULT %s %.6f\n", key, t);
+}
+
+// The uniform row skeletons of two classes of the table's uniform rows: eight
+// waves in one workgroup per CU (256x256x64 w128x64 s2), and four waves in two
+// workgroups per CU (128x128x64 w64x64 s2). A record the model does not read,
+// run only by --uniform-rows-only: scaling those rows' K-steps by these figures
+// predicted the measured sweeps worse.
+bool uniformRows(int cus, float* dSink, const std::vector<uint32_t>& hOperands) {
+    constexpr int kMaxPerCu = 2;  // the most workgroups per CU either skeleton launches
+    Stamp* dStamps = nullptr;
+    CAL_HIP_CHECK(hipMalloc(&dStamps, size_t(cus) * kMaxPerCu * sizeof(Stamp)));
+    std::printf("\nuniform row skeletons: the kernel's K loop on a four-tile L2-resident source, %d K tiles\n",
+                kPersistentTiles);
+    _Float16* dSrc = nullptr;
+    constexpr size_t kSrcBytes = 4 * 64 * 1024;
+    CAL_HIP_CHECK(hipMalloc(&dSrc, kSrcBytes));
+    for (size_t off = 0; off < kSrcBytes; off += 16 * 1024)
+        CAL_HIP_CHECK(hipMemcpy(reinterpret_cast<char*>(dSrc) + off, hOperands.data(), 16 * 1024,
+                                hipMemcpyHostToDevice));
+    bool ok = true;
+    uniformRowStep<256, 256, 64, 128, 64, 2>("uniformRowStepCycles1", cus, 1, dSrc, dSink, dStamps, ok);
+    uniformRowStep<128, 128, 64, 64, 64, 2>("uniformRowStepCycles2", cus, kMaxPerCu, dSrc, dSink, dStamps, ok);
+    CAL_HIP_CHECK(hipFree(dSrc));
+    CAL_HIP_CHECK(hipFree(dStamps));
+    return ok;
+}
+
 // The persistent skeleton of the table's BK = 128 rows (one compute wave per
 // SIMD, 128x64x128 w64x32 s3), reported as persistentStepCycles3: a record the
 // model does not read, run only by --persistent-bk128-only. Its 48 KiB refill per
@@ -733,8 +895,10 @@ bool pingPongRows(int cus, float* dSink, Stamp* dStamps, const std::vector<uint3
 int main(int argc, char** argv) {
     const bool pingPongOnly = argc > 1 && std::string(argv[1]) == "--ping-pong-rows-only";
     const bool deepOnly = argc > 1 && std::string(argv[1]) == "--persistent-bk128-only";
-    if (argc > 1 && !pingPongOnly && !deepOnly) {
-        std::fprintf(stderr, "usage: cal-smem-bw [--ping-pong-rows-only | --persistent-bk128-only]\n");
+    const bool uniformOnly = argc > 1 && std::string(argv[1]) == "--uniform-rows-only";
+    if (argc > 1 && !pingPongOnly && !deepOnly && !uniformOnly) {
+        std::fprintf(stderr,
+                     "usage: cal-smem-bw [--ping-pong-rows-only | --persistent-bk128-only | --uniform-rows-only]\n");
         return 2;
     }
     const hipDeviceProp_t prop = deviceBanner();
@@ -744,11 +908,12 @@ int main(int argc, char** argv) {
     CAL_HIP_CHECK(hipMalloc(&dSink, sizeof(uint32_t)));
     CAL_HIP_CHECK(hipMalloc(&dStamps, cus * sizeof(Stamp)));
     warmUp();
-    if (pingPongOnly || deepOnly) {
+    if (pingPongOnly || deepOnly || uniformOnly) {
         float* dFSink = nullptr;
         CAL_HIP_CHECK(hipMalloc(&dFSink, sizeof(float)));
         const bool ok = pingPongOnly ? pingPongRows(cus, dFSink, dStamps, randomHalfWords())
-                                     : persistentDeep(cus, dFSink, dStamps, randomHalfWords());
+                        : deepOnly   ? persistentDeep(cus, dFSink, dStamps, randomHalfWords())
+                                     : uniformRows(cus, dFSink, randomHalfWords());
         CAL_HIP_CHECK(hipFree(dFSink));
         CAL_HIP_CHECK(hipFree(dSink));
         CAL_HIP_CHECK(hipFree(dStamps));
