@@ -737,3 +737,27 @@ def test_tenth_heldout_figures_as_reported():
     xs = [x for x, _, _ in ratios]
     assert len(xs) == 14 and min(xs) == pytest.approx(1.040, abs=0.001)
     assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.118, abs=0.001)
+
+
+# The eleventh held-out sweep (data/sweep/mi355x-heldout11.md).
+REGISTERED11 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout11-registered.csv")
+FROZEN11 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout11-hw.json")
+TABLE11 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout11-table.csv")
+
+
+def test_eleventh_heldout_registration():
+    """14 shapes from value sets no earlier set could hold, none in an earlier set;
+    the tenth set's table and the tenth set's constants, unchanged."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED11)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, REGISTERED6,
+                 REGISTERED7, REGISTERED8, REGISTERED9, REGISTERED10, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    values = (2304, 3328, 6400, 9728, 12032)
+    assert len(held) == 14 and not held & earlier
+    assert all(M in values and N in values and K in (768, 1408, 2176, 3968) for M, N, K in held)
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE11) == keys(TABLE10) == list(V.kernel_table_keys())
+    assert json.load(open(FROZEN11)) == json.load(open(FROZEN10))
