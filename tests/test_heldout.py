@@ -375,6 +375,8 @@ CURRENT_FIGURES = [
      (6.33, 1.65, 6.95, 0.20)),
     ("mi355x-heldout10.csv", (5.38, 0.36, 3.82, 0.0), (5.70, 1.14, 10.83, 0.0), (6.37, 1.60, 10.07, 0.0),
      (5.52, 0.36, 3.82, 0.0)),
+    ("mi355x-heldout11.csv", (5.10, 1.76, 6.22, 0.03), (5.80, 1.62, 6.62, 0.03), (5.31, 1.76, 6.22, 0.03),
+     (4.79, 1.57, 10.28, 0.03)),
 ]
 
 
@@ -392,8 +394,8 @@ def test_current_model_figures(tmp_path, name, now, no_ping_pong_step, no_mall_w
     under the same constants with pingPongStepModel, mallWriteModel, then
     writeOverlapModel switched off (one at a time).
 
-    Every set but the tenth held-out one was measured before pingPongStepModel
-    existed, so for those 13 these are its in-sample effects: MAPE lower on every set (mean 8.20 against 8.80%); regret
+    Every set but the tenth and eleventh held-out ones was measured before
+    pingPongStepModel existed, so for those 13 these are its in-sample effects: MAPE lower on every set (mean 8.20 against 8.80%); regret
     at k = 1 worst lower on the seventh, eighth and ninth held-out sets (10.16 ->
     1.83, 5.85 -> 5.17, 11.37 -> 4.83%) and the same on the other 10. Without
     pingPongStepModel the figures are those the ninth held-out set was scored with;
@@ -761,3 +763,44 @@ def test_eleventh_heldout_registration():
                          for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
     assert keys(TABLE11) == keys(TABLE10) == list(V.kernel_table_keys())
     assert json.load(open(FROZEN11)) == json.load(open(FROZEN10))
+
+
+MEASURED11 = os.path.join(ROOT, "data", "measured", "mi355x-heldout11.csv")
+
+
+def test_eleventh_heldout_figures_as_reported():
+    """Measured once as registered (canary range 1.0%): MAPE 5.10%, mean Spearman
+    0.928, regret at k = 1 1.76% mean and 6.22% worst (9728 x 6400 x 768), 5 of 14
+    exact; at k = 10 0.03% mean and 0.35% worst, 13 of 14 exact, the first set whose
+    k = 10 shortlist misses a best row. Without pingPongStepModel the same constants
+    give MAPE 5.80% and regret at k = 1 1.62% / 6.62%. The best row beats hipBLASLt on
+    13 of 14 shapes, geometric mean 1.087x, lowest 0.993x (6400 x 3328 x 3968)."""
+    import json
+    import math
+    frozen = T.read(TABLE11, require=V.KEY_COLUMNS)
+    keys = [tuple(frozen.number(i, c, int) for c in V.KEY_COLUMNS) for i in range(len(frozen))]
+    table = T.read(MEASURED11)
+    absent, unexpected = V.registered_gate(table.records, T.read_shapes(REGISTERED11), keys)
+    assert not absent and not unexpected and float(table.meta["canary_drift_fraction"]) <= 0.05
+    assert _figures(MEASURED11, FROZEN11) == pytest.approx((5.10, 1.76, 6.22, 0.03), abs=0.01)
+    result, total, shapes, _ = AT.evaluate(MEASURED11, FROZEN11, ks=(1, 3, 10))
+    by_k = {r["k"]: r for r in result}
+    assert (total, shapes) == (336, 14) and by_k[1]["hits"] == 5
+    assert by_k[3]["hits"] == by_k[10]["hits"] == 13
+    assert by_k[10]["max_regret"] == pytest.approx(0.35, abs=0.01)
+    base = AT.baselines(MEASURED11, FROZEN11, ks=(1, 10))
+    assert base[1]["random"][0] == pytest.approx(16.81, abs=0.01)
+    h = json.load(open(FROZEN11))
+    h["pingPongStepModel"] = 0
+    import tempfile
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        json.dump(h, f)
+    try:
+        assert _figures(MEASURED11, f.name) == pytest.approx((5.80, 1.62, 6.62, 0.03), abs=0.01)
+    finally:
+        os.unlink(f.name)
+    ratios = V.vendor_ratios([MEASURED11])
+    xs = [x for x, _, _ in ratios]
+    assert len(xs) == 14 and sum(x > 1.0 for x in xs) == 13
+    assert min(xs) == pytest.approx(0.993, abs=0.001)
+    assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.087, abs=0.001)
