@@ -47,7 +47,7 @@ figure is the sum of the two predicted launch times; `roofline.traffic` is null
 
 autotune: the metric's second half, the mean top-10 regret of the model-pruned
 autotuner, is computed from the committed measured sweep of the current kernels
-(data/measured/mi355x-steady-loop.csv, 14 shapes x 24 variants; the same sweep with
+(data/measured/mi355x-current-kernels.csv, 14 shapes x 24 variants; the same sweep with
 the previous kernels, data/measured/mi355x.csv, beside it) and the committed
 calibration (data/hardware/mi355x.json)
 by ridge_amd.autotune, with regret at top-1 and the expected regret of a random
@@ -77,7 +77,7 @@ PROFILES = os.path.join(ROOT, "profiles")
 # The in-sample sweep measured with the current kernels, and the same sweep with
 # the kernels before the steady K-loop passes (the set every earlier figure and
 # the held-out comparisons refer to).
-MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-steady-loop.csv")
+MEASURED_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-current-kernels.csv")
 MEASURED_SWEEP_PREVIOUS = os.path.join(ROOT, "data", "measured", "mi355x.csv")
 HARDWARE_JSON = os.path.join(ROOT, "data", "hardware", "mi355x.json")
 HELDOUT_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout.csv")
@@ -287,7 +287,7 @@ def measured_traffic(M, N, K, key, cold=False):
 def autotune_regret(k=10):
     """The pruner's regret at top-1 and top-k with the random-shortlist baseline,
     on the committed in-sample sweep measured with the current kernels
-    (data/measured/mi355x-steady-loop.csv, 14 shapes x 24 variants, current
+    (data/measured/mi355x-current-kernels.csv, 14 shapes x 24 variants, current
     calibration), on the same sweep with the previous kernels
     (data/measured/mi355x.csv) and on the eleven held-out sweeps, each
     registered before it was measured and scored with the constants frozen with

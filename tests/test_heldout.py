@@ -369,6 +369,9 @@ CURRENT_FIGURES = [
     # The in-sample shapes re-measured with the steady-pass kernels.
     ("mi355x-steady-loop.csv", (6.84, 0.70, 5.92, 0.0), (7.30, 0.70, 5.92, 0.0), (8.95, 1.51, 11.40, 0.0),
      (7.54, 3.39, 15.05, 0.05)),
+    # The same shapes re-measured with the current kernels (steady passes and K stagger).
+    ("mi355x-current-kernels.csv", (7.69, 0.48, 2.93, 0.0), (8.30, 0.48, 2.93, 0.0), (9.22, 1.24, 10.59, 0.0),
+     (8.23, 3.47, 17.01, 0.0)),
     ("mi355x-heldout8.csv", (7.18, 0.67, 5.17, 0.0), (7.20, 1.23, 5.85, 0.0), (9.10, 2.55, 19.66, 0.0),
      (6.69, 0.67, 5.17, 0.0)),
     ("mi355x-heldout9.csv", (6.50, 1.17, 4.83, 0.0), (6.95, 1.98, 11.37, 0.0), (7.62, 1.52, 5.28, 0.0),
@@ -394,8 +397,9 @@ def test_current_model_figures(tmp_path, name, now, no_ping_pong_step, no_mall_w
     under the same constants with pingPongStepModel, mallWriteModel, then
     writeOverlapModel switched off (one at a time).
 
-    Every set but the tenth and eleventh held-out ones was measured before
-    pingPongStepModel existed, so for those 13 these are its in-sample effects: MAPE lower on every set (mean 8.20 against 8.80%); regret
+    Every set but the tenth and eleventh held-out ones and the current-kernel
+    re-measurement was measured before pingPongStepModel existed, so for those 13
+    these are its in-sample effects: MAPE lower on every set (mean 8.20 against 8.80%); regret
     at k = 1 worst lower on the seventh, eighth and ninth held-out sets (10.16 ->
     1.83, 5.85 -> 5.17, 11.37 -> 4.83%) and the same on the other 10. Without
     pingPongStepModel the figures are those the ninth held-out set was scored with;
