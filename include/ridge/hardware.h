@@ -144,7 +144,7 @@ struct HardwareModel {
                                      // 1: that max scaled by what the ping-pong row skeleton of the
                                      //    same class measures: its cycles per K tile over the model's
                                      //    max for the skeleton's own row (256x256x32 w128x64 s3 for
-                                     //    BK = 32, 256x128x64 w64x64 s3 for BK = 64)
+                                     //    BK = 32, 256x128x64 w64x64 s3 for BK = 64 and above)
     double pingPongRowStepCycles[2] = {0.0, 0.0};  // [CAL] cycles per K tile of those two skeletons
     int fillShareModel = 0;          // 0: every workgroup fetches its first tiles from HBM (reference)
                                      // 1: the resident workgroups' first tiles come from HBM once per

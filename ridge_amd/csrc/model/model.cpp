@@ -264,8 +264,8 @@ double persistentStepRatio(const GemmConfig& cfg, const HardwareModel& hw, int d
 }
 
 // pingPongStepModel 1: the measured K-step of the ping-pong row skeleton of a
-// row's class (its BK) over the model's max(MFMAs, reads) for the skeleton's
-// own row. The skeletons are cal-smem-bw's: 256x256x32 w128x64 s3 and
+// row's class (BK = 32, or BK of 64 and above) over the model's max(MFMAs,
+// reads) for the skeleton's own row. The skeletons are cal-smem-bw's: 256x256x32 w128x64 s3 and
 // 256x128x64 w64x64 s3, the kernel's phase loop on an L2-resident source.
 double pingPongStepRatio(const GemmConfig& cfg, const HardwareModel& hw, int db) {
     GemmConfig skel = cfg;
