@@ -808,3 +808,27 @@ def test_eleventh_heldout_figures_as_reported():
     assert len(xs) == 14 and sum(x > 1.0 for x in xs) == 13
     assert min(xs) == pytest.approx(0.993, abs=0.001)
     assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.087, abs=0.001)
+
+
+# The twelfth held-out sweep (data/sweep/mi355x-heldout12.md).
+REGISTERED12 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout12-registered.csv")
+FROZEN12 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout12-hw.json")
+TABLE12 = os.path.join(ROOT, "data", "sweep", "mi355x-heldout12-table.csv")
+
+
+def test_twelfth_heldout_registration():
+    """14 shapes from value sets no earlier set could hold, none in an earlier set;
+    the eleventh set's table and constants, unchanged."""
+    import json
+    held = {s[:3] for s in T.read_shapes(REGISTERED12)}
+    earlier = set()
+    for path in (IN_SAMPLE, REGISTERED, REGISTERED2, REGISTERED3, REGISTERED4, REGISTERED5, REGISTERED6,
+                 REGISTERED7, REGISTERED8, REGISTERED9, REGISTERED10, REGISTERED11, BASELINE_SHAPES):
+        earlier |= {s[:3] for s in T.read_shapes(path)}
+    values = (2816, 4352, 5888, 10752, 15104)
+    assert len(held) == 14 and not held & earlier
+    assert all(M in values and N in values and K in (1664, 2432, 3200, 4480) for M, N, K in held)
+    keys = lambda path: [tuple(T.read(path, require=V.KEY_COLUMNS).number(i, c, int) for c in V.KEY_COLUMNS)  # noqa
+                         for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
+    assert keys(TABLE12) == keys(TABLE11) == list(V.kernel_table_keys())
+    assert json.load(open(FROZEN12)) == json.load(open(FROZEN11))
