@@ -51,7 +51,7 @@ autotuner, is computed from the committed measured sweep of the current kernels
 the previous kernels, data/measured/mi355x.csv, beside it) and the committed
 calibration (data/hardware/mi355x.json)
 by ridge_amd.autotune, with regret at top-1 and the expected regret of a random
-shortlist beside it, and the same for the eleven held-out sweeps, each registered
+shortlist beside it, and the same for the twelve held-out sweeps, each registered
 before it was measured and scored with the constants frozen beside it
 (data/measured/mi355x-heldout*.csv); it is a property of the sweeps and the model,
 not of this run's timing.
@@ -102,6 +102,8 @@ HELDOUT10_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout10.csv")
 HELDOUT10_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout10-hw.json")
 HELDOUT11_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout11.csv")
 HELDOUT11_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout11-hw.json")
+HELDOUT12_SWEEP = os.path.join(ROOT, "data", "measured", "mi355x-heldout12.csv")
+HELDOUT12_HARDWARE_JSON = os.path.join(ROOT, "data", "sweep", "mi355x-heldout12-hw.json")
 # Host threads for the CPU baseline: the cores this process may use, capped at
 # the 16 a GPU box grants one GPU.
 MAX_CPU_THREADS = 16
@@ -289,7 +291,7 @@ def autotune_regret(k=10):
     on the committed in-sample sweep measured with the current kernels
     (data/measured/mi355x-current-kernels.csv, 14 shapes x 24 variants, current
     calibration), on the same sweep with the previous kernels
-    (data/measured/mi355x.csv) and on the eleven held-out sweeps, each
+    (data/measured/mi355x.csv) and on the twelve held-out sweeps, each
     registered before it was measured and scored with the constants frozen with
     it (data/measured/mi355x-heldout*.csv); a property of the
     sweeps and the model, not of this run's timing. None of it is computed if
@@ -309,7 +311,8 @@ def autotune_regret(k=10):
                                    ("held_out_8", HELDOUT8_SWEEP, HELDOUT8_HARDWARE_JSON),
                                    ("held_out_9", HELDOUT9_SWEEP, HELDOUT9_HARDWARE_JSON),
                                    ("held_out_10", HELDOUT10_SWEEP, HELDOUT10_HARDWARE_JSON),
-                                   ("held_out_11", HELDOUT11_SWEEP, HELDOUT11_HARDWARE_JSON)):
+                                   ("held_out_11", HELDOUT11_SWEEP, HELDOUT11_HARDWARE_JSON),
+                                   ("held_out_12", HELDOUT12_SWEEP, HELDOUT12_HARDWARE_JSON)):
             table, total, shapes, _ = AT.evaluate(measured, hw, ks=(1, k))
             base = AT.baselines(measured, hw, ks=(1, k))
             by_k = {r["k"]: r for r in table}

@@ -380,6 +380,8 @@ CURRENT_FIGURES = [
      (5.52, 0.36, 3.82, 0.0)),
     ("mi355x-heldout11.csv", (5.10, 1.76, 6.22, 0.03), (5.80, 1.62, 6.62, 0.03), (5.31, 1.76, 6.22, 0.03),
      (4.79, 1.57, 10.28, 0.03)),
+    ("mi355x-heldout12.csv", (3.95, 0.29, 1.82, 0.0), (4.56, 0.63, 6.52, 0.0), (4.45, 0.29, 1.82, 0.0),
+     (4.26, 0.29, 1.82, 0.0)),
 ]
 
 
@@ -397,7 +399,7 @@ def test_current_model_figures(tmp_path, name, now, no_ping_pong_step, no_mall_w
     under the same constants with pingPongStepModel, mallWriteModel, then
     writeOverlapModel switched off (one at a time).
 
-    Every set but the tenth and eleventh held-out ones and the current-kernel
+    Every set but the tenth to twelfth held-out ones and the current-kernel
     re-measurement was measured before pingPongStepModel existed, so for those 13
     these are its in-sample effects: MAPE lower on every set (mean 8.20 against 8.80%); regret
     at k = 1 worst lower on the seventh, eighth and ninth held-out sets (10.16 ->
@@ -832,3 +834,41 @@ def test_twelfth_heldout_registration():
                          for i in range(len(T.read(path, require=V.KEY_COLUMNS)))]
     assert keys(TABLE12) == keys(TABLE11) == list(V.kernel_table_keys())
     assert json.load(open(FROZEN12)) == json.load(open(FROZEN11))
+
+
+MEASURED12 = os.path.join(ROOT, "data", "measured", "mi355x-heldout12.csv")
+
+
+def test_twelfth_heldout_figures_as_reported():
+    """Measured once as registered (canary range 2.0%): MAPE 3.95%, mean Spearman
+    0.955, regret at k = 1 0.29% mean and 1.82% worst, 9 of 14 exact; k = 10 finds
+    every shape's best. Without pingPongStepModel the same constants give MAPE
+    4.56% and regret at k = 1 0.63% / 6.52%. The best row beats hipBLASLt on all 14
+    shapes, geometric mean 1.100x, lowest 1.026x (5888 x 5888 x 1664)."""
+    import json
+    import math
+    frozen = T.read(TABLE12, require=V.KEY_COLUMNS)
+    keys = [tuple(frozen.number(i, c, int) for c in V.KEY_COLUMNS) for i in range(len(frozen))]
+    table = T.read(MEASURED12)
+    absent, unexpected = V.registered_gate(table.records, T.read_shapes(REGISTERED12), keys)
+    assert not absent and not unexpected and float(table.meta["canary_drift_fraction"]) <= 0.05
+    assert _figures(MEASURED12, FROZEN12) == pytest.approx((3.95, 0.29, 1.82, 0.0), abs=0.01)
+    result, total, shapes, _ = AT.evaluate(MEASURED12, FROZEN12, ks=(1, 3, 10))
+    by_k = {r["k"]: r for r in result}
+    assert (total, shapes) == (336, 14) and by_k[1]["hits"] == 9
+    assert by_k[3]["hits"] == 11 and by_k[10]["hits"] == 14
+    base = AT.baselines(MEASURED12, FROZEN12, ks=(1, 10))
+    assert base[1]["random"][0] == pytest.approx(18.51, abs=0.01)
+    h = json.load(open(FROZEN12))
+    h["pingPongStepModel"] = 0
+    import tempfile
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        json.dump(h, f)
+    try:
+        assert _figures(MEASURED12, f.name) == pytest.approx((4.56, 0.63, 6.52, 0.0), abs=0.01)
+    finally:
+        os.unlink(f.name)
+    ratios = V.vendor_ratios([MEASURED12])
+    xs = [x for x, _, _ in ratios]
+    assert len(xs) == 14 and min(xs) == pytest.approx(1.026, abs=0.001)
+    assert math.exp(sum(math.log(x) for x in xs) / len(xs)) == pytest.approx(1.100, abs=0.001)
